@@ -1,0 +1,462 @@
+// AWQ W4A16 group-128 GEMM, skinny-M GEMV and dequantisation for gfx950.
+//
+// Packed layout (awq/qmodule.py:43-99, interleave 4, kstride 64): weight
+// (n, k) lives in qweight row n/4.  The 16 bytes at int16 columns
+// 64*kb + 16*(n%4) + 8*c .. +7 hold the 32 nibbles of row n for
+// k in [64*kb + 32*c, +32) as four little-endian u32 words f = 0..3; nibble
+// i = 4*e + h of word f is k = 64*kb + 32*c + 8*h + 2*f + e.  So one 16-byte
+// load gives one row's full 32-k chunk, and "pair h" of each word -- nibbles
+// (h, h+4) -- is the two consecutive k = 8*h + 2*f + {0,1}.
+//
+// MFMA mapping (v_mfma_f32_16x16x32_{f16,bf16}): A operand = dequantised
+// weights (row i = output channel n), B operand = activations (column j =
+// token m).  Lane (g = lane/16, l = lane%16) feeds 8 k-slots; for k-step t of
+// a 128-k group the slot s of lane group g is k = 32*g + 8*t + s on BOTH
+// operands: activations are read as 8 contiguous halves from LDS, weights are
+// pair t of the lane's four words.  The output lands as lane (g, l) holding
+// out[m = l][n = 4*g + r], r = 0..3: four consecutive channels per lane.
+#include "common.h"
+
+namespace qv {
+
+// ---------------------------------------------------------------- dequant
+// Pair t of word w -> two fp16 weights fp16_rn(q*s + sz), one fused rounding.
+// (w & 0x000f000f) | 0x64006400 is the fp16 pair (1024+q_lo, 1024+q_hi); the
+// 0x00f000f0 mask gives (1024+16q); both are made exact integers q first.
+template <int t>
+__device__ __forceinline__ uint32_t dq_pair_f16(uint32_t w, uint32_t w_hi, f16x2 s2, f16x2 z2) {
+  const uint32_t src = (t < 2) ? w : w_hi;
+  const uint32_t mask = (t & 1) ? 0x00f000f0u : 0x000f000fu;
+  // One v_and_or_b32 (mask from an SGPR, magic from a VGPR: gfx9 VOP3 takes
+  // no literal and one constant-bus operand).
+  uint32_t bits;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(bits) : "v"(src), "s"(mask), "v"(0x64006400u));
+  const f16x2 h = __builtin_bit_cast(f16x2, bits);
+  f16x2 q;
+  if constexpr ((t & 1) == 0) {
+    q = h - (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
+  } else {
+    q = __builtin_elementwise_fma(h, (f16x2){(_Float16)0.0625f, (_Float16)0.0625f},
+                                  (f16x2){(_Float16)-64.0f, (_Float16)-64.0f});
+  }
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, z2));
+}
+
+// bf16: q*s + sz is exact in fp32 for tables built as sz = -bf16(s*z) (at most
+// 13 significant bits), so fp32 FMA then one RNE rounding to bf16 equals the
+// fused bf16 operation of the reference.
+template <int t>
+__device__ __forceinline__ uint32_t dq_pair_bf16(uint32_t w, float s, float z) {
+  const float q0 = (float)((w >> (4 * t)) & 0xFu);
+  const float q1 = (float)((w >> (4 * t + 16)) & 0xFu);
+  const bf16x2 r = {(__bf16)__builtin_fmaf(q0, s, z), (__bf16)__builtin_fmaf(q1, s, z)};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Weight fragment for k-step t: 8 slots = pair t of words 0..3.
+template <bool BF16, int t>
+__device__ __forceinline__ uint4 dq_frag(const uint4& wq, uint32_t s_bits, uint32_t z_bits) {
+  uint4 r;
+  if constexpr (!BF16) {
+    const f16x2 s2 = __builtin_bit_cast(f16x2, s_bits * 0x10001u);
+    const f16x2 z2 = __builtin_bit_cast(f16x2, z_bits * 0x10001u);
+    r.x = dq_pair_f16<t>(wq.x, wq.x >> 8, s2, z2);
+    r.y = dq_pair_f16<t>(wq.y, wq.y >> 8, s2, z2);
+    r.z = dq_pair_f16<t>(wq.z, wq.z >> 8, s2, z2);
+    r.w = dq_pair_f16<t>(wq.w, wq.w >> 8, s2, z2);
+  } else {
+    const float s = __builtin_bit_cast(float, s_bits << 16);
+    const float z = __builtin_bit_cast(float, z_bits << 16);
+    r.x = dq_pair_bf16<t>(wq.x, s, z);
+    r.y = dq_pair_bf16<t>(wq.y, s, z);
+    r.z = dq_pair_bf16<t>(wq.z, s, z);
+    r.w = dq_pair_bf16<t>(wq.w, s, z);
+  }
+  return r;
+}
+
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Byte offset (in u32 units) of the 16-byte chunk (row n, 32-k chunk g of the
+// 128-k group kt) inside qweight.
+__device__ __forceinline__ size_t qw_chunk_u32(int n, int kt, int g, int K) {
+  return (size_t)(n >> 2) * (size_t)(K >> 1) + (size_t)kt * 64 + (g >> 1) * 32 + (n & 3) * 8 +
+         (g & 1) * 4;
+}
+
+template <bool BF16, int EPI>
+__device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, const uint16_t* __restrict__ bias,
+                                                f32x4 v, int m, int n, int N) {
+  float r[4] = {v[0], v[1], v[2], v[3]};
+  if constexpr (EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU) {
+    const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
+    r[0] += to_f32((uint16_t)(b.x & 0xFFFF), BF16);
+    r[1] += to_f32((uint16_t)(b.x >> 16), BF16);
+    r[2] += to_f32((uint16_t)(b.y & 0xFFFF), BF16);
+    r[3] += to_f32((uint16_t)(b.y >> 16), BF16);
+  }
+  if constexpr (EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_GELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = gelu_erf(r[i]);
+  }
+  uint2 o;
+  o.x = pack2<BF16>(r[0], r[1]);
+  o.y = pack2<BF16>(r[2], r[3]);
+  *reinterpret_cast<uint2*>(out + (size_t)m * N + n) = o;
+}
+
+// ------------------------------------------------------------ GEMM kernel
+// Workgroup: 256 threads = 4 waves arranged (BM/WM) x (BN/WN); tile BM x BN,
+// one 128-k group (= one scale row) per main-loop step.  Activations are
+// staged through double-buffered, padded LDS (register prefetch of the next
+// group overlaps the MFMAs of the current one); packed weights go straight
+// from global memory into registers and are dequantised there, so LDS traffic
+// is activations only.
+template <bool BF16, int BM, int BN, int WM, int WN, int EPI>
+__global__ __launch_bounds__(256) void w4a16_gemm_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K,
+    int tiles_n) {
+  constexpr int LDA = 128 + 8;  // halves per LDS row: 16-byte pad breaks bank aliasing
+  constexpr int RM = WM / 16;
+  constexpr int RN = WN / 16;
+  constexpr int WAVES_N = BN / WN;
+  static_assert((BM / WM) * (BN / WN) == 4, "4 waves per workgroup");
+  constexpr int A_CHUNKS = BM * 16 / 256;  // 16-byte chunks per thread per tile
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDA];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int m0 = (lid / tiles_n) * BM;
+  const int n0 = (lid % tiles_n) * BN;
+  const int wm0 = (wave / WAVES_N) * WM;
+  const int wn0 = (wave % WAVES_N) * WN;
+  const int KT = K >> 7;
+  const int K2 = K * 2;  // bytes per activation row = bytes per qweight row
+
+  // Buffer descriptors rebased on this tile: 32-bit offsets, and reads past
+  // the last valid row / channel return zeros (M and N tails need no clamps).
+  const auto rsA = make_rsrc(x + (size_t)m0 * K, (uint64_t)(M - m0) * K2);
+  const auto rsB = make_rsrc(qw + (size_t)(n0 >> 2) * (K >> 1), (uint64_t)((N - n0) >> 2) * K2);
+  const auto rsS = make_rsrc(scales + n0, ((uint64_t)KT * N - n0) * 2);
+  const auto rsZ = make_rsrc(zeros + n0, ((uint64_t)KT * N - n0) * 2);
+  // chunk c of the activation tile is row (tid>>4) + 16c, 16-byte column tid&15
+  const uint32_t a_voff = (uint32_t)((tid >> 4) * K2 + (tid & 15) * 16);
+  // subtile j is rows wn0 + 16j + li: qweight row ((wn0 + li) >> 2) + 4j
+  const int nl = wn0 + li;
+  const uint32_t b_voff =
+      (uint32_t)((nl >> 2) * K2 + ((g >> 1) * 32 + (li & 3) * 8 + (g & 1) * 4) * 4);
+  const uint32_t s_voff = (uint32_t)(nl * 2);
+
+  uint4 a_reg[A_CHUNKS];
+  uint4 b_reg[RN];
+  uint32_t s_reg[RN], z_reg[RN];
+
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int c = 0; c < A_CHUNKS; ++c)
+      a_reg[c] = buf_load16(rsA, a_voff, c * 16 * K2 + kt * 256);
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < A_CHUNKS; ++c) {
+      const int idx = tid + 256 * c;
+      *reinterpret_cast<uint4*>(&As[buf][(idx >> 4) * LDA + (idx & 15) * 8]) = a_reg[c];
+    }
+  };
+  auto load_b = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < RN; ++j) {
+      b_reg[j] = buf_load16(rsB, b_voff, j * 4 * K2 + kt * 256);
+      s_reg[j] = __builtin_amdgcn_raw_buffer_load_b16(rsS, s_voff, kt * N * 2 + j * 32, 0);
+      z_reg[j] = __builtin_amdgcn_raw_buffer_load_b16(rsZ, s_voff, kt * N * 2 + j * 32, 0);
+    }
+  };
+
+  f32x4 acc[RN][RM];
+#pragma unroll
+  for (int j = 0; j < RN; ++j)
+#pragma unroll
+    for (int i = 0; i < RM; ++i) acc[j][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  load_a(0);
+  load_b(0);
+  store_a(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    const bool more = kt + 1 < KT;
+    uint4 bq[RN];
+    uint32_t sq[RN], zq[RN];
+#pragma unroll
+    for (int j = 0; j < RN; ++j) {
+      bq[j] = b_reg[j];
+      sq[j] = s_reg[j];
+      zq[j] = z_reg[j];
+    }
+    if (more) {
+      load_a(kt + 1);
+      load_b(kt + 1);
+    }
+    const uint16_t* Ab = As[buf];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint4 bf[RM];
+#pragma unroll
+      for (int i = 0; i < RM; ++i)
+        bf[i] = *reinterpret_cast<const uint4*>(&Ab[(wm0 + 16 * i + li) * LDA + 32 * g + 8 * t]);
+#pragma unroll
+      for (int j = 0; j < RN; ++j) {
+        uint4 af;
+        switch (t) {
+          case 0: af = dq_frag<BF16, 0>(bq[j], sq[j], zq[j]); break;
+          case 1: af = dq_frag<BF16, 1>(bq[j], sq[j], zq[j]); break;
+          case 2: af = dq_frag<BF16, 2>(bq[j], sq[j], zq[j]); break;
+          default: af = dq_frag<BF16, 3>(bq[j], sq[j], zq[j]); break;
+        }
+#pragma unroll
+        for (int i = 0; i < RM; ++i) acc[j][i] = mfma16<BF16>(af, bf[i], acc[j][i]);
+      }
+    }
+    if (more) store_a(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < RN; ++j) {
+    const int n = n0 + wn0 + 16 * j + 4 * g;
+    if (n >= N) continue;
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+      const int m = m0 + wm0 + 16 * i + li;
+      if (m < M) epilogue_store4<BF16, EPI>(out, bias, acc[j][i], m, n, N);
+    }
+  }
+}
+
+// ------------------------------------------------------------ GEMV kernel
+// One workgroup per 16 output channels; its W waves split the K groups
+// round-robin.  Lane (g, l) dequantises its 32 weights of row n0+l (chunk g)
+// and dots them with the matching 32 activations of every token with
+// v_dot2 (fp16 pairs, fp32 accumulate).  Partial sums are reduced across the
+// four lane groups with cross-lane shuffles and across waves through LDS.
+template <bool BF16, int MMAX>
+__global__ __launch_bounds__(1024) void w4a16_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K, int epi) {
+  __shared__ float red[16][MMAX][16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const int n = blockIdx.x * 16 + li;
+  const int KT = K >> 7;
+
+  float acc[MMAX];
+#pragma unroll
+  for (int m = 0; m < MMAX; ++m) acc[m] = 0.f;
+
+  for (int kt = wave; kt < KT; kt += nwaves) {
+    const uint4 wq = *reinterpret_cast<const uint4*>(qw + qw_chunk_u32(n, kt, g, K));
+    const uint32_t s = scales[(size_t)kt * N + n];
+    const uint32_t z = zeros[(size_t)kt * N + n];
+    uint4 wf[4];
+    wf[0] = dq_frag<BF16, 0>(wq, s, z);
+    wf[1] = dq_frag<BF16, 1>(wq, s, z);
+    wf[2] = dq_frag<BF16, 2>(wq, s, z);
+    wf[3] = dq_frag<BF16, 3>(wq, s, z);
+    const size_t kbase = (size_t)kt * 128 + 32 * g;
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+      if (m < M) {
+        const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)m * K + kbase);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint4 xv = xp[t];
+          const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+          const uint32_t ws[4] = {wf[t].x, wf[t].y, wf[t].z, wf[t].w};
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            if constexpr (BF16) {
+              acc[m] = __builtin_fmaf(__builtin_bit_cast(float, xs[f] << 16),
+                                      __builtin_bit_cast(float, ws[f] << 16), acc[m]);
+              acc[m] = __builtin_fmaf(__builtin_bit_cast(float, xs[f] & 0xFFFF0000u),
+                                      __builtin_bit_cast(float, ws[f] & 0xFFFF0000u), acc[m]);
+            } else {
+              acc[m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, xs[f]),
+                                              __builtin_bit_cast(f16x2, ws[f]), acc[m], false);
+            }
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MMAX; ++m) {
+    acc[m] += __shfl_xor(acc[m], 16);
+    acc[m] += __shfl_xor(acc[m], 32);
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) red[wave][m][li] = acc[m];
+  }
+  __syncthreads();
+  for (int i = tid; i < M * 16; i += blockDim.x) {
+    const int m = i >> 4, l = i & 15;
+    float v = 0.f;
+    for (int w = 0; w < nwaves; ++w) v += red[w][m][l];
+    const int nn = blockIdx.x * 16 + l;
+    if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU) v += to_f32(bias[nn], BF16);
+    if (epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU) v = gelu_erf(v);
+    out[(size_t)m * N + nn] = from_f32<BF16>(v);
+  }
+}
+
+// ---------------------------------------------------------- dequant kernel
+// One thread per (row n, 32-k chunk): writes 32 weights in natural k order.
+template <bool BF16>
+__global__ __launch_bounds__(256) void w4a16_dequant_kernel(
+    const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ zeros, uint16_t* __restrict__ w, int N, int K) {
+  const int chunks_per_row = K >> 5;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)N * chunks_per_row) return;
+  const int n = (int)(idx / chunks_per_row);
+  const int c = (int)(idx % chunks_per_row);
+  const int kt = c >> 2, g = c & 3;
+  const uint4 wq = *reinterpret_cast<const uint4*>(qw + qw_chunk_u32(n, kt, g, K));
+  const uint32_t s = scales[(size_t)kt * N + n];
+  const uint32_t z = zeros[(size_t)kt * N + n];
+  uint4* dst = reinterpret_cast<uint4*>(w + (size_t)n * K + (size_t)c * 32);
+  dst[0] = dq_frag<BF16, 0>(wq, s, z);
+  dst[1] = dq_frag<BF16, 1>(wq, s, z);
+  dst[2] = dq_frag<BF16, 2>(wq, s, z);
+  dst[3] = dq_frag<BF16, 3>(wq, s, z);
+}
+
+// ------------------------------------------------------------- launchers
+template <bool BF16, int BM, int BN, int WM, int WN>
+static int launch_gemm_cfg(const void* x, const void* qw, const void* s, const void* z,
+                           const void* bias, void* out, int M, int N, int K, int epi,
+                           hipStream_t st) {
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const dim3 grid(tiles_m * tiles_n), block(256);
+#define QV_GEMM_ARGS                                                                          \
+  (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,            \
+      (const uint16_t*)bias, (uint16_t*)out, M, N, K, tiles_n
+  switch (epi) {
+    case QV_EPI_NONE:
+      hipLaunchKernelGGL((w4a16_gemm_kernel<BF16, BM, BN, WM, WN, QV_EPI_NONE>), grid, block, 0, st, QV_GEMM_ARGS);
+      break;
+    case QV_EPI_BIAS:
+      hipLaunchKernelGGL((w4a16_gemm_kernel<BF16, BM, BN, WM, WN, QV_EPI_BIAS>), grid, block, 0, st, QV_GEMM_ARGS);
+      break;
+    case QV_EPI_BIAS_GELU:
+      hipLaunchKernelGGL((w4a16_gemm_kernel<BF16, BM, BN, WM, WN, QV_EPI_BIAS_GELU>), grid, block, 0, st, QV_GEMM_ARGS);
+      break;
+    default:
+      hipLaunchKernelGGL((w4a16_gemm_kernel<BF16, BM, BN, WM, WN, QV_EPI_GELU>), grid, block, 0, st, QV_GEMM_ARGS);
+      break;
+  }
+#undef QV_GEMM_ARGS
+  return check_launch("w4a16_gemm");
+}
+
+template <bool BF16>
+static int launch_gemv(const void* x, const void* qw, const void* s, const void* z, const void* bias,
+                       void* out, int M, int N, int K, int epi, hipStream_t st) {
+  const int KT = K / 128;
+  int waves = KT < 16 ? KT : 16;
+  const dim3 grid(N / 16), block(64 * waves);
+#define QV_GEMV(MM)                                                                            \
+  hipLaunchKernelGGL((w4a16_gemv_kernel<BF16, MM>), grid, block, 0, st, (const uint16_t*)x,    \
+                     (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,              \
+                     (const uint16_t*)bias, (uint16_t*)out, M, N, K, epi)
+  if (M <= 1) QV_GEMV(1);
+  else if (M <= 2) QV_GEMV(2);
+  else if (M <= 4) QV_GEMV(4);
+  else if (M <= 8) QV_GEMV(8);
+  else QV_GEMV(16);
+#undef QV_GEMV
+  return check_launch("w4a16_gemv");
+}
+
+static int check_common(const void* x, const void* qw, const void* s, const void* z, const void* bias,
+                        const void* out, int64_t M, int64_t N, int64_t K, int dtype, int epi) {
+  QV_CHECK_ARG(dtype == QV_F16 || dtype == QV_BF16, "unsupported dtype %d (expected fp16 or bf16)", dtype);
+  QV_CHECK_ARG(M >= 0 && N > 0 && K > 0, "bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  QV_CHECK_ARG(K % 128 == 0, "K=%lld must be a multiple of the group size 128", (long long)K);
+  QV_CHECK_ARG(N % 16 == 0, "N=%lld must be a multiple of 16", (long long)N);
+  QV_CHECK_ARG(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX && M * K <= (int64_t)1 << 40, "shape too large");
+  QV_CHECK_ARG(epi >= QV_EPI_NONE && epi <= QV_EPI_GELU, "bad epilogue %d", epi);
+  QV_CHECK_ARG(bias != nullptr || !(epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU), "epilogue needs a bias pointer");
+  QV_CHECK_ARG(M == 0 || (x && qw && s && z && out), "null pointer argument");
+  QV_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)qw % 16) == 0, "x and qweight must be 16-byte aligned");
+  QV_CHECK_ARG(((uintptr_t)out % 8) == 0, "out must be 8-byte aligned");
+  QV_CHECK_ARG(bias == nullptr || ((uintptr_t)bias % 8) == 0, "bias must be 8-byte aligned");
+  return QV_OK;
+}
+
+}  // namespace qv
+
+using namespace qv;
+
+extern "C" int qv_w4a16_gemm(const void* x, const void* qweight, const void* scales,
+                             const void* scaled_zeros, const void* bias, void* out, int64_t M,
+                             int64_t N, int64_t K, int dtype, int epilogue, void* stream) {
+  int rc = check_common(x, qweight, scales, scaled_zeros, bias, out, M, N, K, dtype, epilogue);
+  if (rc) return rc;
+  if (M == 0) return QV_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == QV_BF16)
+    return launch_gemm_cfg<true, 128, 128, 64, 64>(x, qweight, scales, scaled_zeros, bias, out,
+                                                   (int)M, (int)N, (int)K, epilogue, st);
+  return launch_gemm_cfg<false, 128, 128, 64, 64>(x, qweight, scales, scaled_zeros, bias, out,
+                                                  (int)M, (int)N, (int)K, epilogue, st);
+}
+
+extern "C" int qv_w4a16_gemv(const void* x, const void* qweight, const void* scales,
+                             const void* scaled_zeros, const void* bias, void* out, int64_t M,
+                             int64_t N, int64_t K, int group_size, int dtype, int epilogue,
+                             void* stream) {
+  QV_CHECK_ARG(group_size == 128, "unsupported group size %d for the GEMV (only 128)", group_size);
+  QV_CHECK_ARG(M >= 1 && M <= 16, "unsupported batch size M=%lld for the GEMV (1..16)", (long long)M);
+  int rc = check_common(x, qweight, scales, scaled_zeros, bias, out, M, N, K, dtype, epilogue);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == QV_BF16)
+    return launch_gemv<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+  return launch_gemv<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+}
+
+extern "C" int qv_w4a16_dequant(const void* qweight, const void* scales, const void* scaled_zeros,
+                                void* out_w, int64_t N, int64_t K, int dtype, void* stream) {
+  QV_CHECK_ARG(dtype == QV_F16 || dtype == QV_BF16, "unsupported dtype %d", dtype);
+  QV_CHECK_ARG(N > 0 && K > 0 && K % 128 == 0 && N % 4 == 0, "bad shape N=%lld K=%lld", (long long)N, (long long)K);
+  QV_CHECK_ARG(N <= INT32_MAX && K <= INT32_MAX, "shape too large");
+  QV_CHECK_ARG(qweight && scales && scaled_zeros && out_w, "null pointer argument");
+  QV_CHECK_ARG(((uintptr_t)qweight % 16) == 0 && ((uintptr_t)out_w % 16) == 0, "buffers must be 16-byte aligned");
+  const size_t total = (size_t)N * (size_t)(K / 32);
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == QV_BF16)
+    hipLaunchKernelGGL((w4a16_dequant_kernel<true>), grid, block, 0, st, (const uint32_t*)qweight,
+                       (const uint16_t*)scales, (const uint16_t*)scaled_zeros, (uint16_t*)out_w, (int)N, (int)K);
+  else
+    hipLaunchKernelGGL((w4a16_dequant_kernel<false>), grid, block, 0, st, (const uint32_t*)qweight,
+                       (const uint16_t*)scales, (const uint16_t*)scaled_zeros, (uint16_t*)out_w, (int)N, (int)K);
+  return check_launch("w4a16_dequant");
+}

@@ -1,0 +1,183 @@
+"""GPU parity of the W4A16 path against the oracle (oracle/awq.py).
+
+Bars: dequantisation bit-exact; GEMM/GEMV fp16 outputs within
+max|y - y_ref| / max|y_ref| <= 1e-2 of the fp32 dequant reference (the
+tolerance stated for this path), plus absolute error reported.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _to_dev(p, dev, dtype=torch.float16):
+    t = {
+        "x": torch.from_numpy(p["x"]).to(dev),
+        "qweight": torch.from_numpy(p["qweight"]).to(dev),
+        "scales": torch.from_numpy(p["scales"]).to(dev),
+        "scaled_zeros": torch.from_numpy(p["scaled_zeros"]).to(dev),
+    }
+    return t
+
+
+def _bf16_problem(p):
+    """bf16 copy of a problem: scales rounded to bf16, sz = -bf16(s*z)."""
+    N = p["s"].shape[0]
+    K = p["x"].shape[1]
+    s_bits = O.f64_to_bf16_bits(p["s"].astype(np.float64))
+    s = O.bf16_bits_to_f32(s_bits).astype(np.float64)
+    sz_bits = O.f64_to_bf16_bits(-(s * p["z"]))
+    rows = O.scale_rows(K)
+    sc = np.zeros((rows, N), np.uint16)
+    sz = np.zeros((rows, N), np.uint16)
+    sc[: s.shape[1]] = s_bits.T
+    sz[: s.shape[1]] = sz_bits.T
+    x_bits = O.f64_to_bf16_bits(p["x"].astype(np.float64))
+    return x_bits, sc, sz
+
+
+@pytest.mark.parametrize("N,K", [(64, 128), (3072, 1024), (4096, 1024), (1024, 4096)])
+def test_dequant_bit_exact_fp16(gpu, N, K):
+    from qvggt_amd import awq_inference_engine as E
+    p = O.make_w4_problem(1, K, N, seed=N + K)
+    t = _to_dev(p, gpu)
+    W = E.w4a16_dequantize(t["qweight"], t["scales"], t["scaled_zeros"], K)
+    ref = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K)
+    assert np.array_equal(W.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("N,K", [(64, 256), (3072, 1024)])
+def test_dequant_bit_exact_bf16(gpu, N, K):
+    from qvggt_amd import awq_inference_engine as E
+    p = O.make_w4_problem(1, K, N, seed=3)
+    _, sc, sz = _bf16_problem(p)
+    qw = torch.from_numpy(p["qweight"]).to(gpu)
+    sct = torch.from_numpy(sc.view(np.int16)).to(gpu).view(torch.bfloat16)
+    szt = torch.from_numpy(sz.view(np.int16)).to(gpu).view(torch.bfloat16)
+    W = E.w4a16_dequantize(qw, sct, szt, K)
+    ref = O.dequantize_bf16_bits(p["qweight"], sc, sz, N, K)
+    assert np.array_equal(W.cpu().view(torch.int16).numpy().view(np.uint16), ref)
+
+
+def _check_gemm(y, p, N, K, tol=TOL):
+    W = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K)
+    ref = O.gemm_ref(p["x"], W)
+    got = y.float().cpu().numpy().reshape(ref.shape)
+    err = O.rel_err(got, ref)
+    assert np.isfinite(got).all()
+    assert err <= tol, f"rel err {err:.3e}, abs {np.abs(got - ref).max():.3e}"
+    return err
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (1374, 3072, 1024),   # config 1: VGGT qkv on one frame
+    (17, 3072, 1024), (129, 256, 1024), (200, 48, 128), (1, 16, 128), (33, 1024, 4096),
+    (2748, 4096, 1024),
+])
+def test_gemm_forward_cuda_new_parity(gpu, M, N, K):
+    from qvggt_amd import awq_inference_engine as E
+    p = O.make_w4_problem(M, K, N, seed=M + N + K)
+    t = _to_dev(p, gpu)
+    y = E.gemm_forward_cuda_new(t["x"], t["qweight"], t["scales"], t["scaled_zeros"])
+    assert y.shape == (M, N) and y.dtype == torch.float16
+    _check_gemm(y, p, N, K)
+
+
+def test_gemm_mlp_shapes(gpu):
+    """config 2a shapes at full M: fc1 1024->4096 and fc2 4096->1024, M = 10992."""
+    from qvggt_amd import awq_inference_engine as E
+    for (N, K) in [(4096, 1024), (1024, 4096)]:
+        p = O.make_w4_problem(10992, K, N, seed=N)
+        t = _to_dev(p, gpu)
+        y = E.gemm_forward_cuda_new(t["x"], t["qweight"], t["scales"], t["scaled_zeros"])
+        _check_gemm(y, p, N, K)
+
+
+def test_gemm_3d_input_and_determinism(gpu):
+    from qvggt_amd import awq_inference_engine as E
+    p = O.make_w4_problem(2 * 300, 1024, 512, seed=1)
+    t = _to_dev(p, gpu)
+    x3 = t["x"].view(2, 300, 1024)
+    y1 = E.gemm_forward_cuda_new(x3, t["qweight"], t["scales"], t["scaled_zeros"])
+    y2 = E.gemm_forward_cuda_new(x3, t["qweight"], t["scales"], t["scaled_zeros"])
+    assert y1.shape == (2, 300, 512)
+    assert torch.equal(y1, y2), "re-run is not bitwise identical"
+    _check_gemm(y1, p, 512, 1024)
+
+
+def test_gemm_bf16(gpu):
+    from qvggt_amd import awq_inference_engine as E
+    M, N, K = 300, 512, 1024
+    p = O.make_w4_problem(M, K, N, seed=21)
+    xb, sc, sz = _bf16_problem(p)
+    x = torch.from_numpy(xb.view(np.int16)).to(gpu).view(torch.bfloat16).view(M, K)
+    qw = torch.from_numpy(p["qweight"]).to(gpu)
+    sct = torch.from_numpy(sc.view(np.int16)).to(gpu).view(torch.bfloat16)
+    szt = torch.from_numpy(sz.view(np.int16)).to(gpu).view(torch.bfloat16)
+    y = E.gemm_forward_cuda_new(x, qw, sct, szt)
+    W = O.bf16_bits_to_f32(O.dequantize_bf16_bits(p["qweight"], sc, sz, N, K))
+    ref = O.bf16_bits_to_f32(xb) @ W.T
+    err = O.rel_err(y.float().cpu().numpy(), ref)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("m", list(range(1, 8)))
+def test_gemv_forward_cuda_new_parity(gpu, m):
+    from qvggt_amd import awq_inference_engine as E
+    N, K = 3072, 1024
+    p = O.make_w4_problem(m, K, N, seed=m)
+    t = _to_dev(p, gpu)
+    y = E.gemv_forward_cuda_new(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], m, N, K, 128)
+    assert y.shape == (m, N)
+    _check_gemm(y, p, N, K)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 4096), (8, 3072, 1024), (16, 4096, 1024), (12, 64, 128)])
+def test_linear_small_m_routes_and_matches(gpu, M, N, K):
+    from qvggt_amd import awq_inference_engine as E
+    p = O.make_w4_problem(M, K, N, seed=100 + M)
+    t = _to_dev(p, gpu)
+    y = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"])
+    _check_gemm(y, p, N, K)
+
+
+@pytest.mark.parametrize("M", [5, 700])
+def test_epilogues_bias_gelu(gpu, M):
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd._lib import QV_EPI_BIAS, QV_EPI_BIAS_GELU
+    N, K = 1024, 1024
+    p = O.make_w4_problem(M, K, N, seed=M)
+    t = _to_dev(p, gpu)
+    b = (np.random.default_rng(1).standard_normal(N) * 0.5).astype(np.float16)
+    bt = torch.from_numpy(b).to(gpu)
+    W = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K)
+    ref = O.gemm_ref(p["x"], W) + b.astype(np.float32)
+    y = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=bt, epilogue=QV_EPI_BIAS)
+    assert O.rel_err(y.float().cpu().numpy(), ref) <= TOL
+    from math import erf
+    gelu = np.vectorize(lambda v: 0.5 * v * (1 + erf(v / np.sqrt(2))))
+    y = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=bt, epilogue=QV_EPI_BIAS_GELU)
+    assert O.rel_err(y.float().cpu().numpy(), gelu(ref.astype(np.float64))) <= TOL
+
+
+def test_wqlinear_forward(gpu):
+    from qvggt_amd.awq import WQLinear
+    M, N, K = 400, 3072, 1024
+    p = O.make_w4_problem(M, K, N, seed=77)
+    q = WQLinear(4, 128, K, N, True, gpu)
+    q.qweight.copy_(torch.from_numpy(p["qweight"]))
+    q.scales.copy_(torch.from_numpy(p["scales"]))
+    q.scaled_zeros.copy_(torch.from_numpy(p["scaled_zeros"]))
+    b = np.linspace(-1, 1, N).astype(np.float16)
+    q.bias.copy_(torch.from_numpy(b))
+    x = torch.from_numpy(p["x"]).to(gpu)
+    W = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K)
+    ref = O.gemm_ref(p["x"], W) + b.astype(np.float32)
+    for xin in (x, x[:3]):   # GEMM path and GEMV path (M < 8)
+        y = q(xin)
+        assert O.rel_err(y.float().cpu().numpy(), ref[: xin.shape[0]]) <= TOL

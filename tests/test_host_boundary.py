@@ -1,0 +1,126 @@
+"""CPU tests of the boundary: C-ABI exports, host-side validation and the
+``WQLinear`` buffer contract.  No GPU compute is called here."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq as O
+from qvggt_amd import _lib
+from qvggt_amd import awq_inference_engine as E
+from qvggt_amd.awq import WQLinear, calculate_zeros_width, pack_intweight
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(qv_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_symbol():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} missing: run `python -m qvggt_amd.build` first")
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    declared = _declared_symbols()
+    assert declared, "no qv_* declarations found in include/"
+    missing = [n for n in declared if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # every declared symbol has a ctypes signature, and vice versa
+    assert set(declared) == set(_lib.SIGNATURES), set(declared) ^ set(_lib.SIGNATURES)
+    _lib.load()
+    assert b"gfx950" in _lib.load().qv_version()
+
+
+def test_engine_exports_reference_op_names():
+    # pybind.cpp:18-36
+    ref_ops = ["layernorm_forward_cuda", "gemm_forward_cuda", "gemv_forward_cuda",
+               "gemm_forward_cuda_new", "gemv_forward_cuda_new", "rotary_embedding_neox",
+               "single_query_attention", "fused_rope_with_pos_forward_func",
+               "w8a8_gemm_forward_cuda", "w8a8_gemm_fuse_bias_forward_cuda", "invoke_quant",
+               "rms_norm_general", "silu_and_mul", "gelu_and_quant"]
+    for name in ref_ops:
+        assert callable(getattr(E, name)), name
+
+
+def test_gemv_errors_match_reference_messages():
+    x = torch.zeros(8, 256, dtype=torch.float16)
+    qw = torch.zeros(64 // 4, 256, dtype=torch.int16)
+    sc = torch.zeros(8, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="Unsupported batch size"):
+        E.gemv_forward_cuda_new(x, qw, sc, sc, 8, 64, 256, 128)
+    with pytest.raises(RuntimeError, match="Unsupported group size"):
+        E.gemv_forward_cuda_new(x[:2], qw, sc, sc, 2, 64, 256, 64)
+
+
+def test_ops_refuse_cpu_tensors_and_bad_dtypes():
+    x = torch.zeros(16, 256, dtype=torch.float16)
+    qw = torch.zeros(16, 256, dtype=torch.int16)
+    sc = torch.zeros(8, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        E.gemm_forward_cuda_new(x, qw, sc, sc)
+    with pytest.raises(RuntimeError):
+        E.gemm_forward_cuda_new(x.float(), qw, sc, sc)
+
+
+def test_legacy_and_llm_ops_raise_not_implemented():
+    for name in ("gemm_forward_cuda", "gemv_forward_cuda", "single_query_attention"):
+        with pytest.raises(NotImplementedError):
+            getattr(E, name)()
+
+
+def test_missing_library_raises(tmp_path):
+    with pytest.raises(_lib.NativeLibraryError):
+        _lib.load(tmp_path / "nope.so")
+
+
+# ------------------------------------------------------------ WQLinear
+@pytest.mark.parametrize("K,N", [(1024, 3072), (1024, 4096), (4096, 1024), (2048, 8192)])
+def test_wqlinear_buffers_match_reference_shapes(K, N):
+    m = WQLinear(4, 128, K, N, True, "cpu")
+    rows = calculate_zeros_width(K, 128) * 8  # qmodule.py:169-189
+    assert m.qweight.shape == (N // 4, K) and m.qweight.dtype == torch.int16
+    assert m.scales.shape == (rows, N) and m.scales.dtype == torch.float16
+    assert m.scaled_zeros.shape == (rows, N) and m.scaled_zeros.dtype == torch.float16
+    assert m.bias.shape == (N,)
+    assert set(dict(m.named_buffers())) == {"qweight", "scales", "scaled_zeros", "bias"}
+    assert "w_bit=4" in m.extra_repr()
+
+
+def test_wqlinear_rejects_other_bits():
+    with pytest.raises(NotImplementedError):
+        WQLinear(8, 128, 256, 64, False, "cpu")
+
+
+@pytest.mark.parametrize("N,K", [(4, 64), (64, 256), (3072, 1024)])
+def test_product_pack_matches_oracle(N, K):
+    U = np.random.default_rng(N + K).integers(0, 16, size=(N, K))
+    got = pack_intweight(torch.tensor(U), 4, 64).numpy()
+    assert np.array_equal(got, O.pack_intweight(U))
+
+
+def test_from_linear_recovers_integer_weights():
+    N, K = 64, 256
+    rng = np.random.default_rng(0)
+    U = rng.integers(0, 16, size=(N, K))
+    z = rng.integers(0, 16, size=(N, K // 128))
+    s = (rng.integers(1, 64, size=(N, K // 128)) / 1024).astype(np.float16)  # exact in fp16
+    W = (s.astype(np.float32).repeat(128, 1) * (U - z.repeat(128, 1))).astype(np.float16)
+    lin = torch.nn.Linear(K, N, bias=True).half()
+    lin.weight.data = torch.tensor(W)
+    lin.bias.data = torch.arange(N, dtype=torch.float16)
+    q = WQLinear.from_linear(lin, 4, 128, scales=torch.tensor(s), zeros=torch.tensor(z, dtype=torch.float16))
+    assert np.array_equal(O.unpack_intweight(q.qweight.numpy(), N, K), U)
+    sc, sz = O.build_tables(s, z, K)
+    assert np.array_equal(q.scales.numpy(), sc)
+    assert np.array_equal(q.scaled_zeros.numpy(), sz)
+    assert torch.equal(q.bias, lin.bias.data)
+    # init_only returns zero buffers of the right shapes (loader.py:450)
+    e = WQLinear.from_linear(lin, 4, 128, init_only=True)
+    assert e.qweight.shape == q.qweight.shape and not e.qweight.any()
