@@ -64,10 +64,15 @@ def load(path: Path | str | None = None):
         return lib
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Call an entry point; raise RuntimeError with the library's message on failure."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    rc = fn(*args)
     if rc != QV_OK:
-        msg = lib.qv_last_error().decode(errors="replace")
+        msg = load().qv_last_error().decode(errors="replace")
         raise RuntimeError(f"{name} failed ({rc}): {msg}")

@@ -18,6 +18,7 @@ Differences from the reference, all deliberate:
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 
 import torch
@@ -73,6 +74,16 @@ def _stream(dev: torch.device):
     return C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
+_NULLCTX = contextlib.nullcontext()
+
+
+def _device(dev: torch.device):
+    """Device guard; free when ``dev`` is already the current device."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return _NULLCTX
+    return torch.cuda.device(dev)
+
+
 def _contig(t: torch.Tensor) -> torch.Tensor:
     return t if t.is_contiguous() else t.contiguous()
 
@@ -112,7 +123,7 @@ def w4a16_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
         _fail(f"{what}: bias must be ({N},) {x.dtype}")
     if out is None:
         out = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _device(dev):
         args = (_ptr(x), _ptr(_contig(qweight)), _ptr(_contig(scales)), _ptr(_contig(scaled_zeros)),
                 _ptr(bias), _ptr(out))
         if 1 <= M <= 16:
@@ -139,7 +150,7 @@ def gemm_forward_cuda_new(in_feats: torch.Tensor, kernel: torch.Tensor, scales: 
     out = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=dev)
     if M == 0:
         return out
-    with torch.cuda.device(dev):
+    with _device(dev):
         _lib.call("qv_w4a16_gemm", _ptr(x), _ptr(_contig(kernel)), _ptr(_contig(scales)),
                   _ptr(_contig(zeros)), C.c_void_p(0), _ptr(out), M, N, K, dt, QV_EPI_NONE,
                   _stream(dev))
@@ -166,7 +177,7 @@ def gemv_forward_cuda_new(in_feats: torch.Tensor, kernel: torch.Tensor,
     dev = _on_gpu(in_feats, kernel, scaling_factors, zeros, what=what)
     x = _contig(in_feats)
     out = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _device(dev):
         _lib.call("qv_w4a16_gemv", _ptr(x), _ptr(_contig(kernel)), _ptr(_contig(scaling_factors)),
                   _ptr(_contig(zeros)), C.c_void_p(0), _ptr(out), m, n, k, group_size, dt,
                   QV_EPI_NONE, _stream(dev))
@@ -183,7 +194,7 @@ def w4a16_dequantize(kernel: torch.Tensor, scales: torch.Tensor, zeros: torch.Te
     N = kernel.shape[0] * 4
     _check_w4_tables(kernel, scales, zeros, N, K, scales.dtype, what)
     out = torch.empty(N, K, dtype=scales.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _device(dev):
         _lib.call("qv_w4a16_dequant", _ptr(_contig(kernel)), _ptr(_contig(scales)),
                   _ptr(_contig(zeros)), _ptr(out), N, K, dt, _stream(dev))
     return out

@@ -12,6 +12,8 @@
 #include <stddef.h>
 #include <stdio.h>
 #include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "../../include/qvggt_hip.h"
 
@@ -68,9 +70,26 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)from_f32<BF16>(a) | ((uint32_t)from_f32<BF16>(b) << 16);
 }
 
-// Exact-erf GELU, fp32 (torch.nn.GELU() semantics).
+// erf(x) by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7 absolute):
+// erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-x^2),
+// t = 1 / (1 + p x), x >= 0, odd extension.  Branch-free; one rcp and one exp.
+__device__ __forceinline__ float erf_as(float x) {
+  const float ax = __builtin_fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, ax, 1.0f));
+  float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  p *= t;
+  const float e = __builtin_amdgcn_exp2f(-ax * ax * 1.4426950408889634f);
+  const float r = __builtin_fmaf(-p, e, 1.0f);
+  return __builtin_copysignf(r, x);
+}
+
+// GELU with the exact-erf definition of torch.nn.GELU(): 0.5 v (1 + erf(v/sqrt 2)),
+// erf evaluated by erf_as (error far below fp16 output resolution).
 __device__ __forceinline__ float gelu_erf(float v) {
-  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+  return 0.5f * v * (1.0f + erf_as(v * 0.70710678118654752f));
 }
 
 // Raw buffer descriptor (gfx9 dword3 = 32-bit data format) over `bytes`
@@ -83,6 +102,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
   return __builtin_bit_cast(uint4, v);
+}
+
+// ---- asynchronous global -> LDS copies ("LDS DMA") under explicit control.
+// Issued through inline asm so the compiler neither waits for them before
+// unrelated LDS reads nor before barriers: the kernel orders them itself with
+// s_waitcnt vmcnt(n) + lds_barrier().  Each lane's 16 (or 4) bytes land at
+// lds_base + 16*lane (4*lane); M0 carries the wave-uniform LDS base.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                          uint32_t lds_base) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(soff), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                         uint32_t lds_base) {
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(soff), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
+               : "memory");
+}
+// Workgroup barrier that only drains this wave's LDS operations (not its
+// outstanding global loads, which the caller waits for with s_waitcnt).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Map the hardware workgroup id to a logical tile id so that the workgroups

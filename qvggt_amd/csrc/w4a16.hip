@@ -1,118 +1,18 @@
-// AWQ W4A16 group-128 GEMM, skinny-M GEMV and dequantisation for gfx950.
+// AWQ W4A16 group-128 GEMM (small-tile path and dispatcher), skinny-M GEMV
+// and dequantisation for gfx950.  The AWQ-v2 nibble layout and the exact
+// dequantisation are documented in w4a16_common.h; the large-M streamed GEMM
+// lives in w4a16_stream.hip.
 //
-// Packed layout (awq/qmodule.py:43-99, interleave 4, kstride 64): weight
-// (n, k) lives in qweight row n/4.  The 16 bytes at int16 columns
-// 64*kb + 16*(n%4) + 8*c .. +7 hold the 32 nibbles of row n for
-// k in [64*kb + 32*c, +32) as four little-endian u32 words f = 0..3; nibble
-// i = 4*e + h of word f is k = 64*kb + 32*c + 8*h + 2*f + e.  So one 16-byte
-// load gives one row's full 32-k chunk, and "pair h" of each word -- nibbles
-// (h, h+4) -- is the two consecutive k = 8*h + 2*f + {0,1}.
-//
-// MFMA mapping (v_mfma_f32_16x16x32_{f16,bf16}): A operand = dequantised
-// weights (row i = output channel n), B operand = activations (column j =
-// token m).  Lane (g = lane/16, l = lane%16) feeds 8 k-slots; for k-step t of
-// a 128-k group the slot s of lane group g is k = 32*g + 8*t + s on BOTH
-// operands: activations are read as 8 contiguous halves from LDS, weights are
-// pair t of the lane's four words.  The output lands as lane (g, l) holding
-// out[m = l][n = 4*g + r], r = 0..3: four consecutive channels per lane.
-#include "common.h"
+// MFMA mapping of the 128 x 128 kernel (v_mfma_f32_16x16x32_{f16,bf16}):
+// A operand = dequantised weights (row i = output channel n), B operand =
+// activations (column j = token m).  Lane (g = lane/16, l = lane%16) feeds 8
+// k-slots; for k-step t of a 128-k group the slot s of lane group g is
+// k = 32*g + 8*t + s on BOTH operands: activations are read as 8 contiguous
+// halves from LDS, weights are pair t of the lane's four words.  The output
+// lands as lane (g, l) holding out[m = l][n = 4*g + r], r = 0..3.
+#include "w4a16_common.h"
 
 namespace qv {
-
-// ---------------------------------------------------------------- dequant
-// Pair t of word w -> two fp16 weights fp16_rn(q*s + sz), one fused rounding.
-// (w & 0x000f000f) | 0x64006400 is the fp16 pair (1024+q_lo, 1024+q_hi); the
-// 0x00f000f0 mask gives (1024+16q); both are made exact integers q first.
-template <int t>
-__device__ __forceinline__ uint32_t dq_pair_f16(uint32_t w, uint32_t w_hi, f16x2 s2, f16x2 z2) {
-  const uint32_t src = (t < 2) ? w : w_hi;
-  const uint32_t mask = (t & 1) ? 0x00f000f0u : 0x000f000fu;
-  // One v_and_or_b32 (mask from an SGPR, magic from a VGPR: gfx9 VOP3 takes
-  // no literal and one constant-bus operand).
-  uint32_t bits;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(bits) : "v"(src), "s"(mask), "v"(0x64006400u));
-  const f16x2 h = __builtin_bit_cast(f16x2, bits);
-  f16x2 q;
-  if constexpr ((t & 1) == 0) {
-    q = h - (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
-  } else {
-    q = __builtin_elementwise_fma(h, (f16x2){(_Float16)0.0625f, (_Float16)0.0625f},
-                                  (f16x2){(_Float16)-64.0f, (_Float16)-64.0f});
-  }
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, z2));
-}
-
-// bf16: q*s + sz is exact in fp32 for tables built as sz = -bf16(s*z) (at most
-// 13 significant bits), so fp32 FMA then one RNE rounding to bf16 equals the
-// fused bf16 operation of the reference.
-template <int t>
-__device__ __forceinline__ uint32_t dq_pair_bf16(uint32_t w, float s, float z) {
-  const float q0 = (float)((w >> (4 * t)) & 0xFu);
-  const float q1 = (float)((w >> (4 * t + 16)) & 0xFu);
-  const bf16x2 r = {(__bf16)__builtin_fmaf(q0, s, z), (__bf16)__builtin_fmaf(q1, s, z)};
-  return __builtin_bit_cast(uint32_t, r);
-}
-
-// Weight fragment for k-step t: 8 slots = pair t of words 0..3.
-template <bool BF16, int t>
-__device__ __forceinline__ uint4 dq_frag(const uint4& wq, uint32_t s_bits, uint32_t z_bits) {
-  uint4 r;
-  if constexpr (!BF16) {
-    const f16x2 s2 = __builtin_bit_cast(f16x2, s_bits * 0x10001u);
-    const f16x2 z2 = __builtin_bit_cast(f16x2, z_bits * 0x10001u);
-    r.x = dq_pair_f16<t>(wq.x, wq.x >> 8, s2, z2);
-    r.y = dq_pair_f16<t>(wq.y, wq.y >> 8, s2, z2);
-    r.z = dq_pair_f16<t>(wq.z, wq.z >> 8, s2, z2);
-    r.w = dq_pair_f16<t>(wq.w, wq.w >> 8, s2, z2);
-  } else {
-    const float s = __builtin_bit_cast(float, s_bits << 16);
-    const float z = __builtin_bit_cast(float, z_bits << 16);
-    r.x = dq_pair_bf16<t>(wq.x, s, z);
-    r.y = dq_pair_bf16<t>(wq.y, s, z);
-    r.z = dq_pair_bf16<t>(wq.z, s, z);
-    r.w = dq_pair_bf16<t>(wq.w, s, z);
-  }
-  return r;
-}
-
-template <bool BF16>
-__device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c) {
-  if constexpr (BF16) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-}
-
-// Byte offset (in u32 units) of the 16-byte chunk (row n, 32-k chunk g of the
-// 128-k group kt) inside qweight.
-__device__ __forceinline__ size_t qw_chunk_u32(int n, int kt, int g, int K) {
-  return (size_t)(n >> 2) * (size_t)(K >> 1) + (size_t)kt * 64 + (g >> 1) * 32 + (n & 3) * 8 +
-         (g & 1) * 4;
-}
-
-template <bool BF16, int EPI>
-__device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, const uint16_t* __restrict__ bias,
-                                                f32x4 v, int m, int n, int N) {
-  float r[4] = {v[0], v[1], v[2], v[3]};
-  if constexpr (EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU) {
-    const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
-    r[0] += to_f32((uint16_t)(b.x & 0xFFFF), BF16);
-    r[1] += to_f32((uint16_t)(b.x >> 16), BF16);
-    r[2] += to_f32((uint16_t)(b.y & 0xFFFF), BF16);
-    r[3] += to_f32((uint16_t)(b.y >> 16), BF16);
-  }
-  if constexpr (EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_GELU) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = gelu_erf(r[i]);
-  }
-  uint2 o;
-  o.x = pack2<BF16>(r[0], r[1]);
-  o.y = pack2<BF16>(r[2], r[3]);
-  *reinterpret_cast<uint2*>(out + (size_t)m * N + n) = o;
-}
 
 // ------------------------------------------------------------ GEMM kernel
 // Workgroup: 256 threads = 4 waves arranged (BM/WM) x (BN/WN); tile BM x BN,
@@ -120,7 +20,8 @@ __device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, cons
 // staged through double-buffered, padded LDS (register prefetch of the next
 // group overlaps the MFMAs of the current one); packed weights go straight
 // from global memory into registers and are dequantised there, so LDS traffic
-// is activations only.
+// is activations only.  Used for problems too small to fill the GPU with the
+// streamed kernel's 256-wide tiles.
 template <bool BF16, int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(256) void w4a16_gemm_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
@@ -136,7 +37,8 @@ __global__ __launch_bounds__(256) void w4a16_gemm_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDA];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int g = lane >> 4, li = lane & 15;
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int m0 = (lid / tiles_n) * BM;
@@ -375,6 +277,52 @@ static int launch_gemm_cfg(const void* x, const void* qw, const void* s, const v
   return check_launch("w4a16_gemm");
 }
 
+// Tile choice.  Candidates: streamed kernel with BM = 128 / 96 / 64 (x 256)
+// and the 128 x 128 register-staged kernel; two workgroups run per CU (512
+// slots on 256 CUs).  Score = useful fraction of the occupied slot-rounds
+// times a per-tile efficiency prior (larger BM amortises the dequantisation
+// over more MFMAs).  QVGGT_W4_TILE=s128|s96|s64|n128 forces one (tuning).
+static int w4_tile_override() {
+  static int v = [] {
+    const char* e = getenv("QVGGT_W4_TILE");
+    if (!e) return 0;
+    if (!strcmp(e, "s128")) return 1;
+    if (!strcmp(e, "s96")) return 2;
+    if (!strcmp(e, "s64")) return 3;
+    if (!strcmp(e, "n128")) return 4;
+    return 0;
+  }();
+  return v;
+}
+
+static int w4_pick_tile(int M, int N) {
+  const int ov = w4_tile_override();
+  if (ov) return ov;
+  const struct { int id, bm, bn; double prior; } cand[] = {
+      {1, 128, 256, 1.00}, {2, 96, 256, 0.93}, {3, 64, 256, 0.82}, {4, 128, 128, 0.70}};
+  const double slots = 512.0;
+  int best = 4;
+  double best_score = -1.0;
+  for (const auto& c : cand) {
+    const double tiles = (double)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const double rounds = __builtin_ceil(tiles / slots);
+    const double score = ((double)M * N) / (rounds * slots * c.bm * c.bn) * c.prior;
+    if (score > best_score) { best_score = score; best = c.id; }
+  }
+  return best;
+}
+
+template <bool BF16>
+static int launch_gemm(const void* x, const void* qw, const void* s, const void* z, const void* bias,
+                       void* out, int M, int N, int K, int epi, hipStream_t st) {
+  switch (w4_pick_tile(M, N)) {
+    case 1: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 128, st);
+    case 2: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 96, st);
+    case 3: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 64, st);
+    default: return launch_gemm_cfg<BF16, 128, 128, 64, 64>(x, qw, s, z, bias, out, M, N, K, epi, st);
+  }
+}
+
 template <bool BF16>
 static int launch_gemv(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                        void* out, int M, int N, int K, int epi, hipStream_t st) {
@@ -405,6 +353,7 @@ static int check_common(const void* x, const void* qw, const void* s, const void
   QV_CHECK_ARG(bias != nullptr || !(epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU), "epilogue needs a bias pointer");
   QV_CHECK_ARG(M == 0 || (x && qw && s && z && out), "null pointer argument");
   QV_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)qw % 16) == 0, "x and qweight must be 16-byte aligned");
+  QV_CHECK_ARG(((uintptr_t)s % 4) == 0 && ((uintptr_t)z % 4) == 0, "scale tables must be 4-byte aligned");
   QV_CHECK_ARG(((uintptr_t)out % 8) == 0, "out must be 8-byte aligned");
   QV_CHECK_ARG(bias == nullptr || ((uintptr_t)bias % 8) == 0, "bias must be 8-byte aligned");
   return QV_OK;
@@ -422,10 +371,10 @@ extern "C" int qv_w4a16_gemm(const void* x, const void* qweight, const void* sca
   if (M == 0) return QV_OK;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == QV_BF16)
-    return launch_gemm_cfg<true, 128, 128, 64, 64>(x, qweight, scales, scaled_zeros, bias, out,
-                                                   (int)M, (int)N, (int)K, epilogue, st);
-  return launch_gemm_cfg<false, 128, 128, 64, 64>(x, qweight, scales, scaled_zeros, bias, out,
-                                                  (int)M, (int)N, (int)K, epilogue, st);
+    return launch_gemm<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K,
+                             epilogue, st);
+  return launch_gemm<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K,
+                            epilogue, st);
 }
 
 extern "C" int qv_w4a16_gemv(const void* x, const void* qweight, const void* scales,
