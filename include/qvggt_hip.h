@@ -28,6 +28,7 @@ extern "C" {
 
 #define QV_F16 0
 #define QV_BF16 1
+#define QV_F32 2
 
 /* GEMM epilogues (fusion of qmodule.py:367 `out + bias` and the MLP GELU). */
 #define QV_EPI_NONE 0
@@ -77,6 +78,97 @@ int qv_w4a16_gemv(const void* x, const void* qweight, const void* scales,
 int qv_w4a16_dequant(const void* qweight, const void* scales,
                      const void* scaled_zeros, void* out_w, int64_t N,
                      int64_t K, int dtype, void* stream);
+
+/* ------------------------------------------------------------ W8A8 family */
+
+/*
+ * W8A8 GEMM: out[M,N] fp16 = fp16_rn((float(sum_k a[m,k] b[n,k]) * ws[n]) * as[m] (+ bias[n])).
+ * a int8 (M,K), b int8 (N,K), ws fp16 (N), as fp16 (M), bias fp16 (N) or NULL.
+ * Replaces w8a8_gemm_forward_cuda / w8a8_gemm_fuse_bias_forward_cuda
+ * (w8a8/w8a8_gemm_cuda.h:3-4, w8a8_gemm_cuda.cu:564-607, 881-922).
+ * Requires K % 64 == 0, N % 16 == 0.
+ */
+int qv_w8a8_gemm(const int8_t* a, const int8_t* b, const void* wscales, const void* ascales,
+                 const void* bias, void* out, int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * The raw int32 accumulators of qv_w8a8_gemm (same kernel, no epilogue):
+ * out[M,N] int32 = a . b^T.  Exposes dense_kernel0's accumulators
+ * (w8a8_gemm_cuda.cu:609-850) as a bit-exact check.
+ */
+int qv_w8a8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* out, int64_t M, int64_t N,
+                     int64_t K, void* stream);
+
+/*
+ * Per-token int8 quantisation of x (M,D) (dtype QV_F16/QV_BF16/QV_F32):
+ * scale[m] fp16 = amax/127, q = sat(rint(x * 127/amax)).
+ * Replaces invoke_quant (w8a8/quantization.h:2-4, quantization.cu:42-96).
+ */
+int qv_quant_per_token(const void* x, int dtype, int8_t* q, void* scale, int64_t M, int64_t D,
+                       void* stream);
+
+/*
+ * LayerNorm (E[x^2] - mean^2 variance) fused with int8 quantisation.
+ * per_token != 0: scale (M) fp16 is written (amax of the rounded LN / 127);
+ * per_token == 0: scale[0] fp16 is read and beta is ignored.
+ * Replaces rms_norm_general (w8a8/layernorm.h:3-9, layernorm.cu:155-191).
+ */
+int qv_layernorm_quant(const void* x, int dtype, const void* gamma, const void* beta, int8_t* q,
+                       void* scale, float eps, int per_token, int64_t M, int64_t D, void* stream);
+
+/*
+ * tanh-GELU (fp16 arithmetic) fused with per-token int8 quantisation; tmp
+ * receives the fp16 GELU output.  Replaces gelu_and_quant (w8a8/act.h:5-10,
+ * act.cu:22-90).
+ */
+int qv_gelu_quant(const void* x, int8_t* q, void* scale, void* tmp, int64_t M, int64_t D,
+                  void* stream);
+
+/* ------------------------------------------------------- normalisation */
+
+/*
+ * T5 RMSNorm: out = (x * rsqrt(mean(x^2) + eps)) * gamma, fp16 outputs clamped
+ * to +-64504.  Replaces layernorm_forward_cuda (layernorm/layernorm.h:3,
+ * layernorm.cu:31-116).
+ */
+int qv_rmsnorm(const void* x, const void* gamma, void* out, float eps, int64_t M, int64_t D,
+               int dtype, void* stream);
+
+/*
+ * LayerNorm with torch.nn.LayerNorm semantics (fp32 statistics, two-pass
+ * variance, affine).  The VGGT blocks' norm1/norm2; no counterpart in the
+ * reference extension (the model graph lives in the external vggt-hf).
+ */
+int qv_layernorm(const void* x, const void* gamma, const void* beta, void* out, float eps,
+                 int64_t M, int64_t D, int dtype, void* stream);
+
+/* ---------------------------------------------------------------- RoPE */
+
+/*
+ * Rotate-half RoPE on x[S][B][H][D] with arbitrary element strides
+ * (x_strides / out_strides: 4 int64 each, order s,b,h,d) and fp32 angles
+ * freqs[B][S][D2]; dims >= D2 copied.  Replaces
+ * fused_rope_with_pos_forward_func (rope_new/fused_rope_with_pos.h:3-5,
+ * fused_rope_with_pos.cu:19-164).
+ */
+int qv_rope_with_pos(const void* x, const float* freqs, void* out, int dtype, int64_t S,
+                     int64_t B, int64_t H, int64_t D, int64_t D2, const int64_t* x_strides,
+                     const int64_t* out_strides, void* stream);
+
+/*
+ * VGGT 2-D RoPE (head_dim 64: y on dims [0,32), x on [32,64)) applied to the
+ * q and k parts of a fused fp16 qkv buffer (T tokens, token stride
+ * src_token_stride elements, layout [3][H][64] per token).  Results go to
+ * out + t*dst_token_stride + part*dst_part_stride (part 0 = q, 1 = k); out
+ * may alias qkv for in-place use.  positions: int32 (T,2) = (y, x) in
+ * [0, table_rows) (out-of-range values are clamped); cos/sin tables fp32
+ * (table_rows,16).  Built from fused_rope_with_pos semantics
+ * (rope_new/fused_rope_with_pos.cu:19-57); the 2-D split follows VGGT.
+ */
+int qv_rope2d(const void* qkv, void* out, const int32_t* positions, const float* cos_table,
+              const float* sin_table, int64_t table_rows, int64_t T, int64_t H,
+              int64_t src_token_stride, int64_t dst_token_stride, int64_t dst_part_stride,
+              void* stream);
 
 #ifdef __cplusplus
 }

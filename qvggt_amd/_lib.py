@@ -32,6 +32,15 @@ SIGNATURES: dict[str, list] = {
     "qv_w4a16_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp],
     "qv_w4a16_gemv": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp],
     "qv_w4a16_dequant": [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
+    "qv_w8a8_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "qv_w8a8_gemm_i32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "qv_quant_per_token": [_vp, _i32, _vp, _vp, _i64, _i64, _vp],
+    "qv_layernorm_quant": [_vp, _i32, _vp, _vp, _vp, _vp, _f32, _i32, _i64, _i64, _vp],
+    "qv_gelu_quant": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
+    "qv_rmsnorm": [_vp, _vp, _vp, _f32, _i64, _i64, _i32, _vp],
+    "qv_layernorm": [_vp, _vp, _vp, _vp, _f32, _i64, _i64, _i32, _vp],
+    "qv_rope_with_pos": [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
+    "qv_rope2d": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp],
 }
 _RESTYPES = {"qv_last_error": C.c_char_p, "qv_version": C.c_char_p}
 

@@ -222,36 +222,255 @@ def single_query_attention(*args, **kwargs):
 
 
 def rotary_embedding_neox(*args, **kwargs):
-    raise NotImplementedError("rotary_embedding_neox: not built yet")
-
-
-def fused_rope_with_pos_forward_func(*args, **kwargs):
-    raise NotImplementedError("fused_rope_with_pos_forward_func: not built yet")
-
-
-def w8a8_gemm_forward_cuda(*args, **kwargs):
-    raise NotImplementedError("w8a8_gemm_forward_cuda: not built yet")
-
-
-def w8a8_gemm_fuse_bias_forward_cuda(*args, **kwargs):
-    raise NotImplementedError("w8a8_gemm_fuse_bias_forward_cuda: not built yet")
-
-
-def invoke_quant(*args, **kwargs):
-    raise NotImplementedError("invoke_quant: not built yet")
-
-
-def rms_norm_general(*args, **kwargs):
-    raise NotImplementedError("rms_norm_general: not built yet")
-
-
-def gelu_and_quant(*args, **kwargs):
-    raise NotImplementedError("gelu_and_quant: not built yet")
+    """1-D NeoX RoPE from a cos/sin cache (position_embedding/pos_encoding_kernels.cu:5-79):
+    an LLM op outside the VGGT path (VGGT uses 2-D RoPE, see ``rope2d``)."""
+    raise NotImplementedError("rotary_embedding_neox: LLM 1-D RoPE is out of scope for the VGGT path; "
+                              "use fused_rope_with_pos_forward_func or rope2d.")
 
 
 def silu_and_mul(*args, **kwargs):
-    raise NotImplementedError("silu_and_mul: not built yet")
+    """SwiGLU activation (w8a8/act.cu:94-131): an LLM op; the VGGT MLP uses GELU."""
+    raise NotImplementedError("silu_and_mul: SwiGLU is out of scope for the VGGT path (its MLP uses GELU).")
 
 
-def layernorm_forward_cuda(*args, **kwargs):
-    raise NotImplementedError("layernorm_forward_cuda: not built yet")
+# -------------------------------------------------------------- W8A8 ops
+_DT_ANY = {torch.float16: QV_F16, torch.bfloat16: QV_BF16, torch.float32: 2}
+
+
+def _dtype_any(t: torch.Tensor, what: str) -> int:
+    if t.dtype not in _DT_ANY:
+        _fail(f"{what}: unsupported dtype {t.dtype} (expected float32, float16 or bfloat16)")
+    return _DT_ANY[t.dtype]
+
+
+def _need(t: torch.Tensor, dtype, what: str, name: str):
+    if t.dtype != dtype:
+        _fail(f"{what}: {name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        _fail(f"{what}: {name} must be contiguous (it is written in place)")
+
+
+def _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, what):
+    for name, t, dt in (("in_feats", in_feats, torch.int8), ("kernel", kernel, torch.int8),
+                        ("wscales", wscales, torch.float16), ("ascales", ascales, torch.float16),
+                        ("out_feats", out_feats, torch.float16)):
+        _need(t, dt, what, name)
+    if in_feats.dim() != 2 or kernel.dim() != 2:
+        _fail(f"{what}: in_feats and kernel must be 2-D (M,K) and (N,K)")
+    M, K = in_feats.shape
+    N = kernel.shape[0]
+    if kernel.shape[1] != K:
+        _fail(f"{what}: K mismatch {K} vs {kernel.shape[1]}")
+    if out_feats.shape[-2:] != (M, N):
+        _fail(f"{what}: out_feats must be (M, N) = ({M}, {N}), got {tuple(out_feats.shape)}")
+    if wscales.numel() != N or ascales.numel() != M:
+        _fail(f"{what}: wscales must have N={N} and ascales M={M} elements")
+    if bias is not None:
+        _need(bias, torch.float16, what, "bias")
+        if bias.numel() != N:
+            _fail(f"{what}: bias must have N={N} elements")
+    dev = _on_gpu(in_feats, kernel, wscales, ascales, out_feats, bias, what=what)
+    with _device(dev):
+        _lib.call("qv_w8a8_gemm", _ptr(in_feats), _ptr(kernel), _ptr(wscales), _ptr(ascales), _ptr(bias),
+                  _ptr(out_feats), M, N, K, _stream(dev))
+
+
+def w8a8_gemm_forward_cuda(in_feats, kernel, wscales, ascales, out_feats) -> None:
+    """out_feats[M,N] = fp16((float(int8 A . int8 B^T) * ws[n]) * as[m]), written in place
+    (w8a8/w8a8_gemm_cuda.cu:881-922)."""
+    _w8a8(in_feats, kernel, wscales, ascales, out_feats, None, "w8a8_gemm_forward_cuda")
+
+
+def w8a8_gemm_fuse_bias_forward_cuda(in_feats, kernel, wscales, ascales, out_feats, bias) -> None:
+    """As ``w8a8_gemm_forward_cuda`` plus bias[n] (w8a8/w8a8_gemm_cuda.cu:564-607)."""
+    _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, "w8a8_gemm_fuse_bias_forward_cuda")
+
+
+def w8a8_gemm_int32(in_feats: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:
+    """Raw int32 accumulators in_feats (M,K) int8 . kernel (N,K)^T (bit-exact check)."""
+    what = "w8a8_gemm_int32"
+    _need(in_feats, torch.int8, what, "in_feats")
+    _need(kernel, torch.int8, what, "kernel")
+    M, K = in_feats.shape
+    N = kernel.shape[0]
+    dev = _on_gpu(in_feats, kernel, what=what)
+    out = torch.empty(M, N, dtype=torch.int32, device=dev)
+    with _device(dev):
+        _lib.call("qv_w8a8_gemm_i32", _ptr(in_feats), _ptr(kernel), _ptr(out), M, N, K, _stream(dev))
+    return out
+
+
+def invoke_quant(out: torch.Tensor, input: torch.Tensor, scale: torch.Tensor) -> None:
+    """Per-token int8 quantisation (w8a8/quantization.cu:81-96): out int8 like input,
+    scale fp16 (tokens,) = amax/127."""
+    what = "invoke_quant"
+    dt = _dtype_any(input, what)
+    _need(out, torch.int8, what, "out")
+    _need(scale, torch.float16, what, "scale")
+    D = input.shape[-1]
+    M = input.numel() // D if D else 0
+    if out.numel() != input.numel() or scale.numel() < M:
+        _fail(f"{what}: out must match input and scale hold {M} tokens")
+    dev = _on_gpu(out, input, scale, what=what)
+    x = _contig(input)
+    with _device(dev):
+        _lib.call("qv_quant_per_token", _ptr(x), dt, _ptr(out), _ptr(scale), M, D, _stream(dev))
+
+
+def rms_norm_general(out: torch.Tensor, input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                     scaling: torch.Tensor, epsilon: float, use_per_token_quant: bool = True) -> None:
+    """LayerNorm + int8 quantisation (w8a8/layernorm.cu:155-191; despite the name a full
+    LayerNorm with mean and beta).  Per token: scaling (tokens,) fp16 is written; per
+    tensor: scaling[0] fp16 is read and bias is not used."""
+    what = "rms_norm_general"
+    dt = _dtype_any(input, what)
+    _need(out, torch.int8, what, "out")
+    _need(scaling, torch.float16, what, "scaling")
+    D = input.shape[-1]
+    M = input.numel() // D if D else 0
+    if weight.dtype != input.dtype or weight.numel() != D:
+        _fail(f"{what}: weight must be ({D},) {input.dtype}")
+    if use_per_token_quant and (bias is None or bias.dtype != input.dtype or bias.numel() != D):
+        _fail(f"{what}: bias must be ({D},) {input.dtype}")
+    if out.numel() != input.numel() or scaling.numel() < (M if use_per_token_quant else 1):
+        _fail(f"{what}: out must match input; scaling too small")
+    dev = _on_gpu(out, input, weight, bias if use_per_token_quant else None, scaling, what=what)
+    x = _contig(input)
+    with _device(dev):
+        _lib.call("qv_layernorm_quant", _ptr(x), dt, _ptr(_contig(weight)),
+                  _ptr(_contig(bias) if use_per_token_quant else None), _ptr(out), _ptr(scaling),
+                  C.c_float(epsilon), 1 if use_per_token_quant else 0, M, D, _stream(dev))
+
+
+def gelu_and_quant(out: torch.Tensor, input: torch.Tensor, scale_out: torch.Tensor, tmp: torch.Tensor) -> None:
+    """tanh-GELU (fp16 arithmetic) + per-token int8 (w8a8/act.cu:30-90); tmp gets the
+    fp16 GELU values, scale_out the per-token fp16 scales."""
+    what = "gelu_and_quant"
+    if input.dtype != torch.float16:
+        _fail(f"{what}: input must be float16 (the reference kernel is half-only)")
+    _need(out, torch.int8, what, "out")
+    _need(scale_out, torch.float16, what, "scale_out")
+    _need(tmp, torch.float16, what, "tmp")
+    D = input.shape[-1]
+    M = input.numel() // D if D else 0
+    if out.numel() != input.numel() or tmp.numel() != input.numel() or scale_out.numel() < M:
+        _fail(f"{what}: out/tmp must match input, scale_out hold {M} tokens")
+    dev = _on_gpu(out, input, scale_out, tmp, what=what)
+    x = _contig(input)
+    with _device(dev):
+        _lib.call("qv_gelu_quant", _ptr(x), _ptr(out), _ptr(scale_out), _ptr(tmp), M, D, _stream(dev))
+
+
+def layernorm_forward_cuda(_input: torch.Tensor, _gamma: torch.Tensor, _out: torch.Tensor, eps: float) -> None:
+    """T5 RMSNorm (layernorm/layernorm.cu:98-116): input must be 3-D (m = size0*size1,
+    n = size2), out written in place, fp16 outputs clamped to +-64504."""
+    what = "layernorm_forward_cuda"
+    if _input.dim() != 3:
+        _fail(f"{what}: input must be 3-D (got {_input.dim()}-D)")
+    dt = _dtype_code(_input, what)
+    if _gamma.dtype != _input.dtype or _out.dtype != _input.dtype:
+        _fail(f"{what}: gamma and out must have the input dtype {_input.dtype}")
+    _need(_out, _input.dtype, what, "out")
+    M = _input.shape[0] * _input.shape[1]
+    D = _input.shape[2]
+    if _gamma.numel() != D or _out.numel() != _input.numel():
+        _fail(f"{what}: gamma must be ({D},) and out match input")
+    dev = _on_gpu(_input, _gamma, _out, what=what)
+    with _device(dev):
+        _lib.call("qv_rmsnorm", _ptr(_contig(_input)), _ptr(_contig(_gamma)), _ptr(_out), C.c_float(eps),
+                  M, D, dt, _stream(dev))
+
+
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-6,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """torch.nn.LayerNorm semantics over the last dim (fp32 statistics): the VGGT
+    blocks' norm1 / norm2.  No reference op (the model graph is external)."""
+    what = "layer_norm"
+    dt = _dtype_code(x, what)
+    D = x.shape[-1]
+    M = x.numel() // D if D else 0
+    if weight.dtype != x.dtype or bias.dtype != x.dtype or weight.numel() != D or bias.numel() != D:
+        _fail(f"{what}: weight/bias must be ({D},) {x.dtype}")
+    dev = _on_gpu(x, weight, bias, out, what=what)
+    x = _contig(x)
+    if out is None:
+        out = torch.empty_like(x)
+    with _device(dev):
+        _lib.call("qv_layernorm", _ptr(x), _ptr(_contig(weight)), _ptr(_contig(bias)), _ptr(out),
+                  C.c_float(eps), M, D, dt, _stream(dev))
+    return out
+
+
+# ----------------------------------------------------------------- RoPE
+def fused_rope_with_pos_forward_func(input: torch.Tensor, freqs: torch.Tensor,
+                                     transpose_output_memory: bool) -> torch.Tensor:
+    """Rotate-half RoPE on input (s, b, h, d) (any strides) with fp32 angles freqs
+    [b][s][d2] (rope_new/fused_rope_with_pos.cu:122-164).  Output (s, b, h, d), stored
+    as (b, s, h, d) memory when transpose_output_memory."""
+    what = "fused_rope_with_pos_forward_func"
+    dt = _dtype_any(input, what)
+    if input.dim() != 4:
+        _fail(f"{what}: input must be 4-D (s, b, h, d)")
+    if freqs.dtype != torch.float32:
+        _fail(f"{what}: freqs must be float32")
+    s, b, h, d = input.shape
+    d2 = freqs.shape[-1]
+    if freqs.numel() != b * s * d2 or d2 > d or d2 % 2:
+        _fail(f"{what}: freqs must hold b*s*d2 = {b}*{s}*{d2} values, d2 even and <= d")
+    dev = _on_gpu(input, freqs, what=what)
+    if transpose_output_memory:
+        out = torch.empty(b, s, h, d, dtype=input.dtype, device=dev).transpose(0, 1)
+    else:
+        out = torch.empty(s, b, h, d, dtype=input.dtype, device=dev)
+    xs = (C.c_int64 * 4)(*input.stride())
+    os_ = (C.c_int64 * 4)(*out.stride())
+    with _device(dev):
+        _lib.call("qv_rope_with_pos", _ptr(input), _ptr(_contig(freqs)), _ptr(out), dt, s, b, h, d, d2,
+                  xs, os_, _stream(dev))
+    return out
+
+
+def rope2d(qkv: torch.Tensor, positions: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+           heads: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """VGGT 2-D RoPE on the q and k parts of a fused qkv (T, 3*heads*64) fp16 tensor.
+
+    positions int32 (T, 2) = (y, x) (0 = special token, unrotated), tables fp32 (P, 16)
+    from ``rope2d_tables``.  Returns out (T, 2, heads, 64) (rotated q, k); pass
+    ``out=qkv`` to rotate in place.
+    """
+    what = "rope2d"
+    if qkv.dtype != torch.float16 or qkv.shape[-1] != 3 * heads * 64:
+        _fail(f"{what}: qkv must be float16 (T, 3*heads*64)")
+    T = qkv.numel() // qkv.shape[-1]
+    if positions.dtype != torch.int32 or positions.numel() != 2 * T:
+        _fail(f"{what}: positions must be int32 (T, 2)")
+    for t in (cos_table, sin_table):
+        if t.dtype != torch.float32 or t.shape[-1] != 16 or not t.is_contiguous():
+            _fail(f"{what}: tables must be contiguous float32 (P, 16)")
+    dev = _on_gpu(qkv, positions, cos_table, sin_table, out, what=what)
+    if not qkv.is_contiguous():
+        _fail(f"{what}: qkv must be contiguous")
+    if out is None:
+        out = torch.empty(T, 2, heads, 64, dtype=qkv.dtype, device=dev)
+        dst_tok, dst_part = 2 * heads * 64, heads * 64
+    elif out.data_ptr() == qkv.data_ptr():
+        dst_tok, dst_part = 3 * heads * 64, heads * 64
+    else:
+        dst_tok, dst_part = out.stride(0), heads * 64
+    with _device(dev):
+        _lib.call("qv_rope2d", _ptr(qkv), _ptr(out), _ptr(_contig(positions)), _ptr(cos_table),
+                  _ptr(sin_table), cos_table.shape[0], T, heads, 3 * heads * 64, dst_tok, dst_part,
+                  _stream(dev))
+    return out
+
+
+def rope2d_tables(max_position: int, base: float = 100.0, device=None):
+    """fp32 cos/sin tables (P, 16) for VGGT's 2-D RoPE: angle = p * base**(-i/16),
+    i = 0..15, evaluated in float64 and rounded once."""
+    import numpy as np
+    p = np.arange(max_position, dtype=np.float64)[:, None]
+    inv = base ** (-np.arange(16, dtype=np.float64) / 16.0)
+    ang = p * inv[None, :].astype(np.float32).astype(np.float64)
+    c = torch.from_numpy(np.cos(ang).astype(np.float32))
+    s = torch.from_numpy(np.sin(ang).astype(np.float32))
+    return (c.to(device), s.to(device)) if device is not None else (c, s)

@@ -55,9 +55,13 @@ __device__ __forceinline__ float ld_f32(const uint16_t* p) {
   return to_f32(*p, BF16);
 }
 
-// fp32 -> 16-bit float, round to nearest even.
+// fp32 -> 16-bit float, round to nearest even.  The empty asm pins v as an
+// fp32 value: otherwise the backend may fold the multiply that produced it
+// and this conversion into one v_fma_mixlo_f16 (one rounding instead of the
+// fp32-then-fp16 roundings the kernels promise).
 template <bool BF16>
 __device__ __forceinline__ uint16_t from_f32(float v) {
+  asm volatile("" : "+v"(v));
   if constexpr (BF16) {
     return __builtin_bit_cast(uint16_t, (__bf16)v);
   } else {

@@ -1,0 +1,161 @@
+// Rotary position embeddings for gfx950.
+//
+// qv_rope_with_pos: fused_rope_with_pos_forward_func of the reference
+// (rope_new/fused_rope_with_pos.cu:19-164): rotate-half RoPE on the first d2
+// dims of x[s][b][h][:] (arbitrary element strides) with fp32 angles
+// freqs[b][s][0:d2]; dims >= d2 are copied.  cos/sin are evaluated in fp64 and
+// rounded to fp32 (the reference used the fast-math sincosf).
+//
+// qv_rope2d: the VGGT 2-D RoPE on the q and k parts of a fused qkv buffer
+// (tokens, 3, H, 64).  Head dims [0,32) rotate with the token's y position,
+// [32,64) with its x position; inside each half, dims (d, d+16) form the
+// rotate-half pair with frequency index d (0..15).  cos/sin come from fp32
+// tables (positions x 16) built on the host; special tokens carry position 0
+// (cos 1, sin 0: unrotated).  out = x*cos - x_pair*sin (first of the pair),
+// x*cos + x_pair*sin (second), fp32 ops with one rounding each.
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+namespace qv {
+
+template <int DT>
+__device__ __forceinline__ float ld1(const void* p, size_t i) {
+  if constexpr (DT == QV_F32) return reinterpret_cast<const float*>(p)[i];
+  else return to_f32(reinterpret_cast<const uint16_t*>(p)[i], DT == QV_BF16);
+}
+template <int DT>
+__device__ __forceinline__ void st1(void* p, size_t i, float v) {
+  if constexpr (DT == QV_F32) reinterpret_cast<float*>(p)[i] = v;
+  else reinterpret_cast<uint16_t*>(p)[i] = from_f32<DT == QV_BF16>(v);
+}
+
+// One thread per (s, b, h, j): j < d2/2 rotates the pair (j, j + d2/2); the
+// threads with j >= d2/2 copy the pass-through dims.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_with_pos_kernel(
+    const void* __restrict__ x, const float* __restrict__ freqs, void* __restrict__ out, int S, int B, int H,
+    int D, int D2, long sx_s, long sx_b, long sx_h, long sx_d, long so_s, long so_b, long so_h, long so_d,
+    int per_head) {
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  const long total = (long)S * B * H * per_head;
+  if (gid >= total) return;
+  const int j = (int)(gid % per_head);
+  long r = gid / per_head;
+  const int hh = (int)(r % H);
+  r /= H;
+  const int bb = (int)(r % B);
+  const int ss = (int)(r / B);
+  const long xi = ss * sx_s + bb * sx_b + hh * sx_h;
+  const long oi = ss * so_s + bb * so_b + hh * so_h;
+  const int half = D2 / 2;
+  if (j < half) {
+    const float* f = freqs + ((long)bb * S + ss) * D2;
+    const float a = ld1<DT>(x, xi + j * sx_d);
+    const float p = ld1<DT>(x, xi + (j + half) * sx_d);
+    const double th0 = (double)f[j], th1 = (double)f[j + half];
+    const float c0 = (float)cos(th0), s0 = (float)sin(th0);
+    const float c1 = (float)cos(th1), s1 = (float)sin(th1);
+    st1<DT>(out, oi + j * so_d, a * c0 + (-p) * s0);
+    st1<DT>(out, oi + (j + half) * so_d, p * c1 + a * s1);
+  } else {
+    for (int d = D2 + (j - half); d < D; d += per_head - half)
+      st1<DT>(out, oi + d * so_d, ld1<DT>(x, xi + d * sx_d));
+  }
+}
+
+// VGGT 2-D RoPE.  One thread per (token, part in {q,k}, head, half, sub):
+// it owns dims base..base+7 and their partners base+16..base+23 with
+// base = 32*half + 8*sub, frequency indices 8*sub .. 8*sub+7.
+__global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                     const int* __restrict__ pos, const float* __restrict__ cos_t,
+                                                     const float* __restrict__ sin_t, int P, int T, int H,
+                                                     long src_tok, long dst_tok, long dst_part) {
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  const long per_tok = 2L * H * 4;
+  if (gid >= (long)T * per_tok) return;
+  const int tok = (int)(gid / per_tok);
+  int r = (int)(gid % per_tok);
+  const int sub = r & 1;
+  const int half = (r >> 1) & 1;
+  const int head = (r >> 2) % H;
+  const int part = (r >> 2) / H;
+  // positions outside the table are clamped (never read out of bounds);
+  // callers keep them in [0, P)
+  int p = pos[2 * tok + half];
+  p = p < 0 ? 0 : (p >= P ? P - 1 : p);
+  const int base = 32 * half + 8 * sub;
+  const uint16_t* s = src + (size_t)tok * src_tok + (size_t)part * H * 64 + (size_t)head * 64 + base;
+  uint16_t* d = dst + (size_t)tok * dst_tok + (size_t)part * dst_part + (size_t)head * 64 + base;
+  const f16x8 a = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(s));
+  const f16x8 b = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(s + 16));
+  const float4* cp = reinterpret_cast<const float4*>(cos_t + (size_t)p * 16 + 8 * sub);
+  const float4* sp = reinterpret_cast<const float4*>(sin_t + (size_t)p * 16 + 8 * sub);
+  const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+  const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  f16x8 oa, ob;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float xa = (float)a[e], xb = (float)b[e];
+    oa[e] = (_Float16)(xa * cs[e] - xb * sn[e]);
+    ob[e] = (_Float16)(xb * cs[e] + xa * sn[e]);
+  }
+  *reinterpret_cast<uint4*>(d) = __builtin_bit_cast(uint4, oa);
+  *reinterpret_cast<uint4*>(d + 16) = __builtin_bit_cast(uint4, ob);
+}
+
+}  // namespace qv
+
+using namespace qv;
+
+extern "C" int qv_rope_with_pos(const void* x, const float* freqs, void* out, int dtype, int64_t S, int64_t B,
+                                int64_t H, int64_t D, int64_t D2, const int64_t* x_strides,
+                                const int64_t* out_strides, void* stream) {
+  QV_CHECK_ARG(S >= 0 && B >= 0 && H >= 0 && D > 0, "bad shape");
+  QV_CHECK_ARG(D2 > 0 && D2 <= D && D2 % 2 == 0, "rotary dim d2=%lld must be even and <= d=%lld", (long long)D2,
+               (long long)D);
+  QV_CHECK_ARG(x_strides && out_strides, "null stride array");
+  if (S * B * H == 0) return QV_OK;
+  QV_CHECK_ARG(x && freqs && out, "null pointer argument");
+  const int half = (int)(D2 / 2);
+  // rotating threads (one per pair) + up to 64 copy threads for dims >= d2
+  const int extra = D > D2 ? (int)(D - D2 < 64 ? D - D2 : 64) : 0;
+  const int per_head = half + extra;
+  const long total = (long)S * B * H * per_head;
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  const long* xs = (const long*)x_strides;
+  const long* os = (const long*)out_strides;
+#define QV_ROPE(DTV)                                                                                        \
+  hipLaunchKernelGGL((rope_with_pos_kernel<DTV>), grid, block, 0, st, x, freqs, out, (int)S, (int)B, (int)H, \
+                     (int)D, (int)D2, xs[0], xs[1], xs[2], xs[3], os[0], os[1], os[2], os[3], per_head)
+  switch (dtype) {
+    case QV_F16: QV_ROPE(QV_F16); break;
+    case QV_BF16: QV_ROPE(QV_BF16); break;
+    case QV_F32: QV_ROPE(QV_F32); break;
+    default: set_error("unsupported dtype %d", dtype); return QV_EINVAL;
+  }
+#undef QV_ROPE
+  return check_launch("rope_with_pos");
+}
+
+extern "C" int qv_rope2d(const void* qkv, void* out, const int32_t* positions, const float* cos_table,
+                         const float* sin_table, int64_t table_rows, int64_t T, int64_t H,
+                         int64_t src_token_stride, int64_t dst_token_stride, int64_t dst_part_stride,
+                         void* stream) {
+  QV_CHECK_ARG(T >= 0 && H > 0, "bad shape T=%lld H=%lld", (long long)T, (long long)H);
+  QV_CHECK_ARG(table_rows > 0 && table_rows <= INT32_MAX, "bad table size %lld", (long long)table_rows);
+  if (T == 0) return QV_OK;
+  QV_CHECK_ARG(qkv && out && positions && cos_table && sin_table, "null pointer argument");
+  QV_CHECK_ARG(src_token_stride % 8 == 0 && dst_token_stride % 8 == 0 && dst_part_stride % 8 == 0 &&
+                   ((uintptr_t)qkv % 16) == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)cos_table % 16) == 0 &&
+                   ((uintptr_t)sin_table % 16) == 0,
+               "rope2d needs 16-byte aligned rows and tables");
+  const long total = T * 2 * H * 4;
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  hipLaunchKernelGGL(rope2d_kernel, grid, block, 0, (hipStream_t)stream, (const uint16_t*)qkv, (uint16_t*)out,
+                     positions, cos_table, sin_table, (int)table_rows, (int)T, (int)H, (long)src_token_stride,
+                     (long)dst_token_stride, (long)dst_part_stride);
+  return check_launch("rope2d");
+}

@@ -1,0 +1,218 @@
+// W8A8 GEMM for gfx950: int8 activations (per-token scale) x int8 weights
+// (per-output-channel scale), exact int32 accumulation on
+// v_mfma_i32_32x32x32_i8, epilogue fp16_rn((float(acc) * ws[n]) * as[m] (+ bias[n])).
+// Replaces dense_kernel0 / dense_kernel0_fuse_bias of the reference
+// (w8a8/w8a8_gemm_cuda.cu:284-607, 609-922).
+//
+// Workgroup tile BM (= 32*MT, m) x 256 (n); the 4 waves sit side by side along
+// n, each owning BM x 64 = MT x 2 MFMA tiles of 32x32.  Activations and
+// weights stream global -> LDS with direct buffer loads through 3 stages of
+// 64 k (A: BM x 64 B, B: 256 x 64 B).  Rows are 64 B = four 16-byte chunks;
+// chunk c of row r is stored at c ^ f(r), f(r) = ((r >> 1) + (r >> 3)) & 3,
+// which keeps every 8- and 16-lane group of a b128 read on distinct banks.
+// K-slots: k-step s (0..1) of a stage, lane half h: k = 32*s + 16*h + 0..15
+// (16 contiguous bytes = chunk 2s + h) on both operands.  Output: lane (h, l),
+// register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the wave's tile.
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+namespace qv {
+
+__device__ __forceinline__ int f8(int r) { return ((r >> 1) + (r >> 3)) & 3; }
+
+template <int MT, int OUT>  // OUT: 0 = fp16 (scaled), 1 = fp16 (scaled + bias), 2 = raw int32
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b,
+                      const uint16_t* __restrict__ ws, const uint16_t* __restrict__ as,
+                      const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
+                      int tiles_n) {
+  constexpr int BM = 32 * MT, BN = 256, NT = 2;
+  constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int NSTAGE = 3;
+  constexpr int A_INSTR = BM / 64;   // 1 KB direct loads per wave per stage (A)
+  constexpr int B_INSTR = 4;         // 16 KB / 1 KB / 4 waves
+  constexpr int VM_PER_STAGE = A_INSTR + B_INSTR;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int m0 = (lid / tiles_n) * BM;
+  const int n0 = (lid % tiles_n) * BN;
+  const int KS = K >> 6;
+
+  const auto rsA = make_rsrc(a + (size_t)m0 * K, (uint64_t)(M - m0) * K);
+  const auto rsB = make_rsrc(b + (size_t)n0 * K, (uint64_t)(N - n0) * K);
+
+  // Direct loads: instruction covers 16 rows r0..r0+15 (r0 % 16 == 0); lane L
+  // lands at row r0 + L/4, physical chunk L%4 = logical c ^ f(row), and
+  // f(r0 + L/4) = ((L >> 3) + (L >> 5) + 2*((r0 >> 4) & 1)) & 3.
+  uint32_t voff[2];
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    const int c = (lane & 3) ^ (((lane >> 3) + (lane >> 5) + 2 * v) & 3);
+    voff[v] = (uint32_t)((lane >> 2) * K + c * 16);
+  }
+  const uint32_t lds0 = lds_addr(lds);
+  auto issue = [&](int ks, int st) {
+    const uint32_t base = lds0 + st * STAGE;
+#pragma unroll
+    for (int q = 0; q < A_INSTR; ++q) {
+      const int r0 = 16 * (A_INSTR * wave + q);
+      lds_dma16(rsA, voff[(r0 >> 4) & 1], r0 * K + ks * 64, base + r0 * 64);
+    }
+#pragma unroll
+    for (int q = 0; q < B_INSTR; ++q) {
+      const int r0 = 16 * (B_INSTR * wave + q);
+      lds_dma16(rsB, voff[(r0 >> 4) & 1], r0 * K + ks * 64, base + A_BYTES + r0 * 64);
+    }
+  };
+
+  i32x16 acc[NT][MT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0;
+
+  const int fl = f8(l32);  // f(32*i + l32) == f(l32) for every i, and f(64*w + 32*j + l32) too
+  auto compute = [&](int st) {
+    const uint8_t* base = lds + st * STAGE;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t col = (uint32_t)(((2 * s + h) ^ fl) * 16);
+      uint4 bw[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        bw[j] = *reinterpret_cast<const uint4*>(base + A_BYTES + (64 * wave + 32 * j + l32) * 64 + col);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const uint4 av = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 64 + col);
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bw[j]),
+                                                            __builtin_bit_cast(i32x4, av), acc[j][i], 0, 0, 0);
+      }
+    }
+  };
+
+  issue(0, 0);
+  if (KS > 1) issue(1, 1);
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks + 1 < KS) {
+      __builtin_amdgcn_s_waitcnt(0x0F70 | VM_PER_STAGE);  // vmcnt(VM_PER_STAGE)
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);                 // vmcnt(0)
+    }
+    lds_barrier();
+    if (ks + 2 < KS) issue(ks + 2, (ks + 2) % NSTAGE);
+    compute(ks % NSTAGE);
+  }
+
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int n = n0 + 64 * wave + 32 * j + 8 * qd + 4 * h;
+      if (n >= N) continue;
+      float wsn[4], bn[4] = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (OUT != 2) {
+        const uint2 wv = *reinterpret_cast<const uint2*>(ws + n);
+        wsn[0] = to_f32((uint16_t)(wv.x & 0xFFFF), false);
+        wsn[1] = to_f32((uint16_t)(wv.x >> 16), false);
+        wsn[2] = to_f32((uint16_t)(wv.y & 0xFFFF), false);
+        wsn[3] = to_f32((uint16_t)(wv.y >> 16), false);
+        if constexpr (OUT == 1) {
+          const uint2 bv = *reinterpret_cast<const uint2*>(bias + n);
+          bn[0] = to_f32((uint16_t)(bv.x & 0xFFFF), false);
+          bn[1] = to_f32((uint16_t)(bv.x >> 16), false);
+          bn[2] = to_f32((uint16_t)(bv.y & 0xFFFF), false);
+          bn[3] = to_f32((uint16_t)(bv.y >> 16), false);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = m0 + 32 * i + l32;
+        if (m >= M) continue;
+        if constexpr (OUT == 2) {
+          int4 o = make_int4(acc[j][i][4 * qd], acc[j][i][4 * qd + 1], acc[j][i][4 * qd + 2], acc[j][i][4 * qd + 3]);
+          *reinterpret_cast<int4*>(reinterpret_cast<int32_t*>(out) + (size_t)m * N + n) = o;
+        } else {
+          const float am = to_f32(as[m], false);
+          float r[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float t = (float)acc[j][i][4 * qd + e] * wsn[e];
+            t = t * am;
+            if constexpr (OUT == 1) t = t + bn[e];
+            // keep the fp32 rounding of t: without this the backend fuses the last
+            // multiply and the fp16 conversion into one v_fma_mixlo_f16 (one rounding)
+            asm volatile("" : "+v"(t));
+            r[e] = t;
+          }
+          uint2 o;
+          o.x = pack2<false>(r[0], r[1]);
+          o.y = pack2<false>(r[2], r[3]);
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + (size_t)m * N + n) = o;
+        }
+      }
+    }
+  }
+}
+
+template <int MT, int OUT>
+static void launch(const void* a, const void* b, const void* ws, const void* as, const void* bias, void* out,
+                   int M, int N, int K, hipStream_t st) {
+  const int tiles_m = (M + 32 * MT - 1) / (32 * MT), tiles_n = (N + 255) / 256;
+  hipLaunchKernelGGL((w8a8_gemm_kernel<MT, OUT>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
+                     (const int8_t*)a, (const int8_t*)b, (const uint16_t*)ws, (const uint16_t*)as,
+                     (const uint16_t*)bias, out, M, N, K, tiles_n);
+}
+
+static int w8a8_run(const void* a, const void* b, const void* ws, const void* as, const void* bias, void* out,
+                    int64_t M, int64_t N, int64_t K, int mode, void* stream) {
+  QV_CHECK_ARG(M >= 0 && N > 0 && K > 0, "bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  QV_CHECK_ARG(K % 64 == 0, "K=%lld must be a multiple of 64", (long long)K);
+  QV_CHECK_ARG(N % 16 == 0, "N=%lld must be a multiple of 16", (long long)N);
+  QV_CHECK_ARG(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "shape too large");
+  QV_CHECK_ARG((uint64_t)N * K < (1ull << 32) && (uint64_t)128 * K < (1ull << 31), "weight too large for 32-bit offsets");
+  if (M == 0) return QV_OK;
+  QV_CHECK_ARG(a && b && out && (mode == 2 || (ws && as)) && (mode != 1 || bias), "null pointer argument");
+  QV_CHECK_ARG(((uintptr_t)a % 16) == 0 && ((uintptr_t)b % 16) == 0, "a and b must be 16-byte aligned");
+  QV_CHECK_ARG(((uintptr_t)out % 16) == 0, "out must be 16-byte aligned");
+  QV_CHECK_ARG(mode == 2 || ((uintptr_t)ws % 8) == 0, "wscales must be 8-byte aligned");
+  QV_CHECK_ARG(mode != 1 || ((uintptr_t)bias % 8) == 0, "bias must be 8-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const long big_tiles = (long)((M + 127) / 128) * ((N + 255) / 256);
+  const bool big = big_tiles >= 256;
+#define QV_W8(MT)                                                                        \
+  switch (mode) {                                                                        \
+    case 0: launch<MT, 0>(a, b, ws, as, bias, out, (int)M, (int)N, (int)K, st); break;   \
+    case 1: launch<MT, 1>(a, b, ws, as, bias, out, (int)M, (int)N, (int)K, st); break;   \
+    default: launch<MT, 2>(a, b, ws, as, bias, out, (int)M, (int)N, (int)K, st); break;  \
+  }
+  if (big) {
+    QV_W8(4)
+  } else {
+    QV_W8(2)
+  }
+#undef QV_W8
+  return check_launch("w8a8_gemm");
+}
+
+}  // namespace qv
+
+extern "C" int qv_w8a8_gemm(const int8_t* a, const int8_t* b, const void* wscales, const void* ascales,
+                            const void* bias, void* out, int64_t M, int64_t N, int64_t K, void* stream) {
+  return qv::w8a8_run(a, b, wscales, ascales, bias, out, M, N, K, bias ? 1 : 0, stream);
+}
+
+extern "C" int qv_w8a8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* out, int64_t M, int64_t N, int64_t K,
+                                void* stream) {
+  return qv::w8a8_run(a, b, nullptr, nullptr, nullptr, out, M, N, K, 2, stream);
+}

@@ -1,0 +1,190 @@
+"""GPU parity of the W8A8, normalisation and RoPE ops against the oracle.
+
+Bars: int32 accumulators, int8 codes, per-token scales and every fp16 output
+of the row kernels bit-exact (the kernels and oracle/w8a8.py share the
+arithmetic contract and reduction order); fused_rope_with_pos within one
+fp16 ulp (its cos/sin of arbitrary fp32 angles go through fp64 library calls
+on both sides); rope2d bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import rope as R
+from oracle import w8a8 as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy()
+    return t.numpy()
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ----------------------------------------------------------- quantisation
+@pytest.mark.parametrize("M,D,dt", [(1374, 1024, np.float16), (10992, 1024, np.float16), (300, 4096, np.float32),
+                                    (5, 8, np.float16), (64, 8192, np.float16)])
+def test_invoke_quant_bit_exact(gpu, M, D, dt):
+    from qvggt_amd import awq_inference_engine as E
+    x = (_rng(M + D).standard_normal((M, D)) * 3).astype(dt)
+    x[0] = 0  # amax = 0 row
+    xt = torch.from_numpy(x).to(gpu)
+    q = torch.empty(M, D, dtype=torch.int8, device=gpu)
+    s = torch.empty(M, dtype=torch.float16, device=gpu)
+    E.invoke_quant(q, xt, s)
+    qr, sr = Q.quant_per_token(x)
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+
+
+# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("M,N,K", [(10992, 4096, 1024), (10992, 1024, 4096), (300, 3072, 1024), (1, 48, 64),
+                                   (37, 272, 192)])
+def test_w8a8_int32_bit_exact(gpu, M, N, K):
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(M * 7 + N)
+    a = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    b = np.clip(np.rint(rng.standard_normal((N, K)) * 32), -128, 127).astype(np.int8)
+    acc = E.w8a8_gemm_int32(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu))
+    assert np.array_equal(acc.cpu().numpy(), Q.w8a8_int32(a, b))
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("M,N,K", [(2748, 4096, 1024), (129, 1024, 4096)])
+def test_w8a8_gemm_fp16_bit_exact(gpu, M, N, K, bias):
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(M + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    a, as_ = Q.quant_per_token(x)
+    b = np.clip(np.rint(rng.standard_normal((N, K)) * 32), -128, 127).astype(np.int8)
+    ws = rng.uniform(0.001, 0.01, N).astype(np.float16)
+    bb = (rng.standard_normal(N) * 0.1).astype(np.float16) if bias else None
+    out = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    args = [torch.from_numpy(v).to(gpu) for v in (a, b, ws, as_)] + [out]
+    if bias:
+        E.w8a8_gemm_fuse_bias_forward_cuda(*args, torch.from_numpy(bb).to(gpu))
+    else:
+        E.w8a8_gemm_forward_cuda(*args)
+    ref = Q.w8a8_epilogue(Q.w8a8_int32(a, b), ws, as_, bb)
+    assert np.array_equal(_bits(out), ref.view(np.int16))
+
+
+# ------------------------------------------------------- LN + quant
+@pytest.mark.parametrize("M,D", [(10992, 1024), (33, 4096), (7, 1000)])
+def test_rms_norm_general_per_token_bit_exact(gpu, M, D):
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(M + D)
+    x = (rng.standard_normal((M, D)) * 2 + 0.5).astype(np.float16)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float16)
+    b = (0.1 * rng.standard_normal(D)).astype(np.float16)
+    q = torch.empty(M, D, dtype=torch.int8, device=gpu)
+    s = torch.empty(M, dtype=torch.float16, device=gpu)
+    E.rms_norm_general(q, torch.from_numpy(x).to(gpu), torch.from_numpy(g).to(gpu), torch.from_numpy(b).to(gpu),
+                       s, 1e-6, True)
+    qr, sr = Q.layernorm_quant(x, g, b, 1e-6)
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+
+
+def test_rms_norm_general_per_tensor_bit_exact(gpu):
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(9)
+    M, D = 500, 1024
+    x = rng.standard_normal((M, D)).astype(np.float16)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float16)
+    sc = np.array([24.0], np.float16)
+    q = torch.empty(M, D, dtype=torch.int8, device=gpu)
+    E.rms_norm_general(q, torch.from_numpy(x).to(gpu), torch.from_numpy(g).to(gpu), None,
+                       torch.from_numpy(sc).to(gpu), 1e-6, False)
+    assert np.array_equal(q.cpu().numpy(), Q.layernorm_quant_per_tensor(x, g, 1e-6, sc[0]))
+
+
+@pytest.mark.parametrize("M,D", [(2748, 4096), (3, 64)])
+def test_gelu_and_quant_bit_exact(gpu, M, D):
+    from qvggt_amd import awq_inference_engine as E
+    x = (_rng(M) .standard_normal((M, D)) * 2).astype(np.float16)
+    q = torch.empty(M, D, dtype=torch.int8, device=gpu)
+    s = torch.empty(M, dtype=torch.float16, device=gpu)
+    tmp = torch.empty(M, D, dtype=torch.float16, device=gpu)
+    E.gelu_and_quant(q, torch.from_numpy(x).to(gpu), s, tmp)
+    qr, sr, tr = Q.gelu_and_quant(x)
+    assert np.array_equal(_bits(tmp), tr.view(np.int16))
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+    assert np.array_equal(q.cpu().numpy(), qr)
+
+
+# ------------------------------------------------------- normalisation
+@pytest.mark.parametrize("shape", [(4, 300, 1024), (2, 7, 4096), (1, 1, 64)])
+def test_layernorm_forward_cuda_rmsnorm_bit_exact(gpu, shape):
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(sum(shape))
+    x = rng.standard_normal(shape).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, shape[-1]).astype(np.float16)
+    out = torch.empty(shape, dtype=torch.float16, device=gpu)
+    E.layernorm_forward_cuda(torch.from_numpy(x).to(gpu), torch.from_numpy(g).to(gpu), out, 1e-6)
+    ref = Q.rmsnorm(x.reshape(-1, shape[-1]), g, 1e-6).reshape(shape)
+    assert np.array_equal(_bits(out), ref.view(np.int16))
+
+
+@pytest.mark.parametrize("M", [10992, 1374, 1])
+def test_vggt_layer_norm_bit_exact(gpu, M):
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(M)
+    D = 1024
+    x = (rng.standard_normal((M, D)) * 1.5 + 0.3).astype(np.float16)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float16)
+    b = (0.1 * rng.standard_normal(D)).astype(np.float16)
+    y = E.layer_norm(torch.from_numpy(x).to(gpu), torch.from_numpy(g).to(gpu), torch.from_numpy(b).to(gpu), 1e-6)
+    assert np.array_equal(_bits(y), Q.layernorm(x, g, b, 1e-6).view(np.int16))
+
+
+# ------------------------------------------------------------------ RoPE
+@pytest.mark.parametrize("transpose_out", [False, True])
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_fused_rope_with_pos(gpu, transpose_out, dt):
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(3)
+    S, B, H, D, D2 = 37, 3, 16, 64, 48
+    base = rng.standard_normal((B, S, H, D)).astype(np.float32)
+    freqs = rng.uniform(-20, 20, (B, S, D2)).astype(np.float32)
+    xt = torch.from_numpy(base).to(gpu).to(dt).transpose(0, 1)   # (S,B,H,D), non-contiguous
+    y = E.fused_rope_with_pos_forward_func(xt, torch.from_numpy(freqs).to(gpu), transpose_out)
+    assert y.shape == (S, B, H, D)
+    ref = R.rope_with_pos(xt.cpu().numpy(), freqs)
+    got = y.cpu().numpy()
+    if dt == torch.float16:
+        ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
+        assert (np.abs(got.astype(np.float32) - ref.astype(np.float32)) <= ulp).all()
+        assert (got == ref).mean() > 0.999
+    else:
+        assert np.abs(got - ref).max() <= 2e-6 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_rope2d_bit_exact(gpu, inplace):
+    from qvggt_amd import awq_inference_engine as E
+    S, H = 2, 16
+    pos = R.vggt_positions(S)
+    T = pos.shape[0]
+    qkv = _rng(4).standard_normal((T, 3 * H * 64)).astype(np.float16)
+    c, s = R.rope2d_tables(38)
+    ct, st = E.rope2d_tables(38, device=gpu)
+    assert np.array_equal(ct.cpu().numpy(), c) and np.array_equal(st.cpu().numpy(), s)
+    qt = torch.from_numpy(qkv).to(gpu)
+    pt = torch.from_numpy(pos).to(gpu)
+    if inplace:
+        E.rope2d(qt, pt, ct, st, H, out=qt)
+        got = qt.view(T, 3, H, 64)[:, :2].cpu().numpy()
+        assert np.array_equal(qt.view(T, 3, H, 64)[:, 2].cpu().numpy(), qkv.reshape(T, 3, H, 64)[:, 2])
+    else:
+        got = E.rope2d(qt, pt, ct, st, H).cpu().numpy()
+    x = qkv.reshape(T, 3, H, 64)
+    for part in range(2):
+        ref = R.rope2d(x[:, part], pos, c, s)
+        assert np.array_equal(got[:, part].view(np.int16), ref.view(np.int16))

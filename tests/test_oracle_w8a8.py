@@ -1,0 +1,182 @@
+"""Pins oracle/w8a8.py and oracle/rope.py with independent checks: known
+answers, float64 closed forms, exact-sum references and brute force."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import rope as R
+from oracle import w8a8 as Q
+
+
+# ------------------------------------------------------------ rounding
+def test_sat_s8_known_answers():
+    v = np.array([0.5, 1.5, 2.5, -0.5, -1.5, 127.4, 127.5, 200.0, -128.5, -300.0, np.nan, np.inf, -np.inf])
+    assert Q.sat_s8(v).tolist() == [0, 2, 2, 0, -2, 127, 127, 127, -128, -128, 0, 127, -128]
+
+
+def test_quant_known_answers():
+    amax = 3.0
+    k = np.arange(-127, 128)
+    x = np.zeros((1, 256), np.float32)
+    x[0, :255] = k * (amax / 127.0)
+    x[0, 255] = amax
+    q, s = Q.quant_per_token(x)
+    assert np.array_equal(q[0, :255], k.astype(np.int8))
+    assert q[0, 255] == 127
+    assert s[0] == np.float16(np.float32(amax) / np.float32(127))
+    # all-zero row: scale 0, codes 0 (0 * inf is NaN -> 0)
+    q0, s0 = Q.quant_per_token(np.zeros((2, 16), np.float16))
+    assert not q0.any() and not s0.any()
+
+
+def test_quant_roundtrip_error_bound():
+    x = np.random.default_rng(0).standard_normal((64, 1024)).astype(np.float16)
+    q, s = Q.quant_per_token(x)
+    amax = np.abs(x.astype(np.float64)).max(axis=1, keepdims=True)
+    err = np.abs(q * (amax / 127.0) - x.astype(np.float64))
+    assert (err <= amax / 127.0 * 0.5 * (1 + 1e-5)).all()
+
+
+# ------------------------------------------------------- reductions
+def test_row_sum_order_close_to_fsum():
+    rng = np.random.default_rng(1)
+    for D in (8, 1024, 4096, 1000 * 8):
+        v = rng.standard_normal((4, D)).astype(np.float32)
+        got = Q.row_sum_f32(v)
+        for r in range(4):
+            exact = math.fsum(v[r].astype(np.float64))
+            assert abs(got[r] - exact) <= 1e-6 * np.abs(v[r]).sum()
+
+
+def test_row_sum_order_is_the_lane_tree():
+    # chunk c of 8 goes to lane c % 64; a sum whose rounding depends on order:
+    v = np.zeros((1, 1024), np.float32)
+    v[0, 0] = 1e8      # lane 0, first element
+    v[0, 8] = 1.0      # lane 1
+    v[0, 512] = -1e8   # lane 0, second pass (chunk 64)
+    # lane 0 sums 1e8 + (-1e8) = 0 exactly, lane 1 holds 1 -> total 1
+    assert Q.row_sum_f32(v)[0] == 1.0
+
+
+# ------------------------------------------------------- normalisations
+def _ln64(x, g, b, eps):
+    x = x.astype(np.float64)
+    m = x.mean(1, keepdims=True)
+    v = ((x - m) ** 2).mean(1, keepdims=True)
+    return (x - m) / np.sqrt(v + eps) * g + b
+
+
+def test_layernorm_matches_float64():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((32, 1024)).astype(np.float16)
+    g = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float16)
+    b = (0.1 * rng.standard_normal(1024)).astype(np.float16)
+    y = Q.layernorm(x, g, b, 1e-6).astype(np.float64)
+    ref = _ln64(x, g.astype(np.float64), b.astype(np.float64), 1e-6)
+    assert np.abs(y - ref).max() <= 2 ** -10 * np.abs(ref).max()
+    # identity affine: zero mean, unit variance (up to fp16)
+    y1 = Q.layernorm(x, np.ones(1024, np.float16), np.zeros(1024, np.float16)).astype(np.float64)
+    assert np.abs(y1.mean(1)).max() < 2e-3 and np.abs(y1.std(1) - 1).max() < 2e-3
+
+
+def test_layernorm_quant_matches_float64_and_bounds():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((16, 1024)).astype(np.float16)
+    g = (1 + 0.1 * rng.standard_normal(1024)).astype(np.float16)
+    b = (0.1 * rng.standard_normal(1024)).astype(np.float16)
+    q, s = Q.layernorm_quant(x, g, b, 1e-6)
+    ref = _ln64(x, g.astype(np.float64), b.astype(np.float64), 1e-6)
+    amax = np.abs(ref).max(1, keepdims=True)
+    assert np.abs(s.astype(np.float64)[:, None] - amax / 127).max() <= 1e-3 * amax.max()
+    # half an LSB per row, plus slack for amax being taken over fp16-rounded values
+    assert (np.abs(q * (amax / 127) - ref) <= 0.55 * amax / 127).all()
+    assert np.abs(q).max(1).min() >= 126   # the largest magnitude maps to +-127
+
+
+def test_rmsnorm_matches_float64_and_clamps():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((8, 512)).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, 512).astype(np.float16)
+    y = Q.rmsnorm(x, g, 1e-6).astype(np.float64)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-6) * g
+    assert np.abs(y - ref).max() <= 2 ** -10 * np.abs(ref).max()
+    xb = np.zeros((1, 64), np.float16)
+    xb[0, 0], xb[0, 1] = 8, -8          # rms = sqrt(128/64); y = +-8/sqrt(2)*60000 overflows fp16
+    big = Q.rmsnorm(xb, np.full(64, 60000, np.float16), 1e-6)
+    assert float(big[0, 0]) == float(np.float16(64504.0)) == -float(big[0, 1])
+    assert np.isfinite(big.astype(np.float32)).all()
+
+
+# ------------------------------------------------------------- GELU
+def test_gelu_fast_close_to_closed_form():
+    x = np.linspace(-6, 6, 4097).astype(np.float16)
+    y = Q.gelu_fast_f16(x).astype(np.float64)
+    ref = Q.gelu_tanh_f64(x.astype(np.float64))
+    assert np.abs(y - ref).max() <= 8e-3 * max(1.0, np.abs(ref).max())
+    assert Q.gelu_fast_f16(np.array([0.0], np.float16))[0] == 0
+
+
+def test_gelu_and_quant_scale_semantics():
+    x = np.random.default_rng(5).standard_normal((4, 256)).astype(np.float16)
+    q, s, tmp = Q.gelu_and_quant(x)
+    amax = np.abs(tmp.astype(np.float32)).max(1)
+    assert np.array_equal(s, (amax / np.float32(127)).astype(np.float16))
+    assert (np.abs(q).max(1) == 127).all()
+
+
+# ------------------------------------------------------------- GEMM
+def test_w8a8_int32_brute_force_and_epilogue():
+    rng = np.random.default_rng(6)
+    a = rng.integers(-128, 128, (5, 64)).astype(np.int8)
+    b = rng.integers(-128, 128, (7, 64)).astype(np.int8)
+    acc = Q.w8a8_int32(a, b)
+    for m in range(5):
+        for n in range(7):
+            assert acc[m, n] == sum(int(a[m, k]) * int(b[n, k]) for k in range(64))
+    ws = rng.uniform(0.001, 0.01, 7).astype(np.float16)
+    as_ = rng.uniform(0.001, 0.05, 5).astype(np.float16)
+    y = Q.w8a8_epilogue(acc, ws, as_).astype(np.float64)
+    ref = acc * ws.astype(np.float64)[None] * as_.astype(np.float64)[:, None]
+    assert np.abs(y - ref).max() <= 2 ** -10 * np.abs(ref).max()
+    # extreme accumulators stay exact in int32
+    big = np.full((1, 4096), -128, np.int8)
+    assert Q.w8a8_int32(big, big)[0, 0] == 4096 * 128 * 128
+
+
+# ------------------------------------------------------------- RoPE
+def test_rope_with_pos_pairs_rotate_like_complex_numbers():
+    rng = np.random.default_rng(7)
+    S, B, H, D, D2 = 5, 3, 2, 40, 32
+    x = rng.standard_normal((S, B, H, D)).astype(np.float32)
+    f = rng.uniform(-5, 5, (B, S, D2 // 2)).astype(np.float32)
+    freqs = np.concatenate([f, f], axis=-1)
+    y = R.rope_with_pos(x, freqs).astype(np.float64)
+    z = (x[..., :16] + 1j * x[..., 16:32]).astype(np.complex128)
+    th = f.transpose(1, 0, 2)[:, :, None, :].astype(np.float64)
+    ref = z * np.exp(1j * th)
+    assert np.abs(y[..., :16] - ref.real).max() < 1e-5
+    assert np.abs(y[..., 16:32] - ref.imag).max() < 1e-5
+    assert np.array_equal(y[..., 32:], x[..., 32:])
+    # zero angles: identity
+    assert np.array_equal(R.rope_with_pos(x, np.zeros((B, S, D2), np.float32)), x)
+
+
+def test_rope2d_is_two_1d_ropes_and_specials_unrotated():
+    rng = np.random.default_rng(8)
+    T, H = 42, 3
+    x = rng.standard_normal((T, H, 64)).astype(np.float16)
+    pos = R.vggt_positions(1, grid=6, specials=6)
+    c, s = R.rope2d_tables(8)
+    y = R.rope2d(x, pos, c, s)
+    assert np.array_equal(y[:6], x[:6])           # position 0 = identity
+    for half in range(2):
+        p = pos[:, half]
+        ang = np.arccos(np.clip(c[p], -1, 1)).astype(np.float64)
+        ang = np.where(s[p] < 0, -ang, ang)
+        fr = np.concatenate([ang, ang], axis=-1).astype(np.float32)   # (T, 32)
+        sub = x[:, :, 32 * half:32 * half + 32].transpose(0, 1, 2)[:, None]  # (T,1,H,32)
+        ref = R.rope_with_pos(sub.astype(np.float32), fr[None].transpose(0, 1, 2).reshape(1, T, 32))
+        assert np.abs(ref[:, 0].astype(np.float64) - y[:, :, 32 * half:32 * half + 32]).max() < 2e-3
+    assert pos.shape == (42, 2) and pos[:6].sum() == 0 and pos[6:].min() == 1
