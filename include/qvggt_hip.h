@@ -170,6 +170,24 @@ int qv_rope2d(const void* qkv, void* out, const int32_t* positions, const float*
               int64_t src_token_stride, int64_t dst_token_stride, int64_t dst_part_stride,
               void* stream);
 
+/* ----------------------------------------------------------- attention */
+
+/*
+ * Flash attention, fp16 in/out, fp32 softmax/accumulation, no mask:
+ * for each of B sequences of L tokens and each of H heads,
+ * out = softmax(q k^T * scale) v with head_dim 64 (the only size supported).
+ * q/k/v/out are token-major with the given token strides (elements) and head
+ * stride 64, so q, k, v can point into a fused (tokens, 3, H, 64) buffer.
+ * VGGT frame attention is B = frames, L = 1374; global attention B = 1,
+ * L = frames * 1374.  No counterpart in the reference extension (its
+ * single_query_attention is an LLM decode kernel, out of scope; VGGT's SDPA
+ * lives in the external vggt-hf).
+ */
+int qv_attention_fwd(const void* q, const void* k, const void* v, void* out, int64_t B,
+                     int64_t L, int64_t H, int64_t head_dim, int64_t q_token_stride,
+                     int64_t k_token_stride, int64_t v_token_stride, int64_t out_token_stride,
+                     float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -474,3 +474,35 @@ def rope2d_tables(max_position: int, base: float = 100.0, device=None):
     c = torch.from_numpy(np.cos(ang).astype(np.float32))
     s = torch.from_numpy(np.sin(ang).astype(np.float32))
     return (c.to(device), s.to(device)) if device is not None else (c, s)
+
+
+# ------------------------------------------------------------- attention
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_len: int, scale: float = 0.125,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """Flash attention over sequences of ``seq_len`` tokens (no mask).
+
+    q, k, v: (T, H, 64) fp16 views with head stride 64 and unit dim stride (any
+    token stride, e.g. ``qkv.view(T, 3, H, 64)[:, i]``); T = B * seq_len.
+    Returns out (T, H, 64) contiguous.  VGGT frame attention: seq_len = 1374
+    (one frame per sequence); global attention: seq_len = T.
+    """
+    what = "attention"
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != torch.float16 or t.dim() != 3 or t.shape[-1] != 64:
+            _fail(f"{what}: {name} must be float16 (T, H, 64)")
+        if t.stride(-1) != 1 or t.stride(-2) != 64:
+            _fail(f"{what}: {name} must have unit dim stride and head stride 64")
+    T, H, _ = q.shape
+    if k.shape != q.shape or v.shape != q.shape:
+        _fail(f"{what}: q, k, v shapes differ")
+    if seq_len <= 0 or T % seq_len:
+        _fail(f"{what}: T={T} is not a multiple of seq_len={seq_len}")
+    dev = _on_gpu(q, k, v, out, what=what)
+    if out is None:
+        out = torch.empty(T, H, 64, dtype=torch.float16, device=dev)
+    elif out.dtype != torch.float16 or out.shape != (T, H, 64) or out.stride(-1) != 1 or out.stride(-2) != 64:
+        _fail(f"{what}: out must be float16 (T, H, 64) with head stride 64")
+    with _device(dev):
+        _lib.call("qv_attention_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(out), T // seq_len, seq_len, H, 64,
+                  q.stride(0), k.stride(0), v.stride(0), out.stride(0), C.c_float(scale), _stream(dev))
+    return out

@@ -1,0 +1,240 @@
+// Flash attention (fp16 in/out, fp32 softmax and accumulation, head_dim 64,
+// no mask) for VGGT's frame and global attention on gfx950.
+//
+// Sequences: B sequences of L tokens each (frame attention: B = frames,
+// L = 1374; global attention: B = 1, L = frames * 1374).  q/k/v/out are
+// token-major with arbitrary token strides and head stride 64, so q, k and v
+// can be read straight out of the fused qkv projection output.
+//
+// Workgroup: 4 waves, 32 queries each (128 queries of one (sequence, head)).
+// Per 64-key tile a wave computes S^T = K Q^T (2 x 4 v_mfma_f32_32x32x16_f16),
+// the online softmax in registers, and O^T += V^T P^T (2 x 4 more MFMAs):
+//  * S^T layout: lane (h = lane/32, q = lane%32) holds, for key block kb,
+//    keys 32kb + 8*(r/4) + 4h + r%4 (r = 0..15) of query q.  A query's 64
+//    scores are split between lanes q and q+32: one cross-lane exchange per
+//    max / sum.
+//  * P^T is the PV B operand without any shuffle: k-step s = 2kb + p takes
+//    registers 8p..8p+7 of block kb, i.e. keys 32kb + 16p + {0..3, 8..11} + 4h.
+//  * V^T (the A operand) is kept transposed in LDS ([dim][key], 136-byte
+//    rows) so each lane reads its 8 keys as two 8-byte loads.
+//  * K tiles arrive by LDS DMA ([key][dim], 128-byte rows, 16-byte chunk c of
+//    row r at c ^ (r & 7) ^ ((r >> 3) & 1)); V tiles are register-staged one
+//    tile ahead and written transposed.
+#include "common.h"
+
+namespace qv {
+
+constexpr int ATT_BQ = 128;   // queries per workgroup
+constexpr int ATT_BK = 64;    // keys per tile
+constexpr int VT_PITCH = 136; // bytes per V^T row (64 keys + 8 B pad)
+
+__device__ __forceinline__ int fk(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+__global__ __launch_bounds__(256) void attention_fwd_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    uint16_t* __restrict__ out, int L, int H, long q_ts, long kv_ts, long v_ts, long o_ts, float scale_log2) {
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][ATT_BK * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[2][64 * VT_PITCH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+  const int qtiles = (L + ATT_BQ - 1) / ATT_BQ;
+  const int bid = blockIdx.x;
+  const int qt = bid % qtiles;
+  const int head = (bid / qtiles) % H;
+  const int seq = bid / (qtiles * H);
+  const long tok0 = (long)seq * L;
+
+  // ---- Q^T fragments (B operand of S^T = K Q^T): 4 k-steps of 16 dims
+  const int qi = qt * ATT_BQ + wave * 32 + l32;     // query index in the sequence
+  const int qc = qi < L ? qi : L - 1;
+  uint4 qf[4];
+  {
+    const uint16_t* qp = q + (tok0 + qc) * q_ts + (long)head * 64;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const uint4*>(qp + 16 * s + 8 * h);
+  }
+
+  // ---- K tile DMA: 8 x 1 KB per tile, 2 per wave; lane L lands at key
+  // r0 + L/8, physical chunk L%8, so it fetches logical chunk (L%8) ^ fk(row).
+  const auto rsK = make_rsrc(k + tok0 * kv_ts + (long)head * 64, (uint64_t)L * kv_ts * 2);
+  uint32_t k_voff[2];
+#pragma unroll
+  for (int w2 = 0; w2 < 2; ++w2) {
+    const int row = 8 * (2 * wave + w2) + (lane >> 3);
+    const int c = (lane & 7) ^ fk(row);
+    k_voff[w2] = (uint32_t)((lane >> 3) * kv_ts * 2 + c * 16);
+  }
+  const uint32_t klds0 = lds_addr(k_lds);
+  auto issue_k = [&](int tile, int buf) {
+#pragma unroll
+    for (int w2 = 0; w2 < 2; ++w2) {
+      const int r0 = 8 * (2 * wave + w2);
+      lds_dma16(rsK, k_voff[w2], (uint32_t)((tile * ATT_BK + r0) * kv_ts * 2),
+                klds0 + buf * (ATT_BK * 128) + r0 * 128);
+    }
+  };
+  // ---- V tile staging: thread t owns keys 2*(t/8), +1 and dims 8*(t%8)..+7
+  const int vkp = tid >> 3, vdg = tid & 7;
+  const auto rsV = make_rsrc(v + tok0 * v_ts + (long)head * 64, (uint64_t)L * v_ts * 2);
+  uint4 vreg[2];
+  auto load_v = [&](int tile) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      vreg[e] = buf_load16(rsV, (uint32_t)(((tile * ATT_BK + 2 * vkp + e) * v_ts + 8 * vdg) * 2), 0);
+  };
+  auto store_vt = [&](int buf) {
+    const uint32_t* a = reinterpret_cast<const uint32_t*>(&vreg[0]);
+    const uint32_t* b = reinterpret_cast<const uint32_t*>(&vreg[1]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t lo = (e & 1) ? (a[e >> 1] >> 16) : (a[e >> 1] & 0xFFFF);
+      const uint32_t hi = (e & 1) ? (b[e >> 1] >> 16) : (b[e >> 1] & 0xFFFF);
+      *reinterpret_cast<uint32_t*>(&vt_lds[buf][(8 * vdg + e) * VT_PITCH + 4 * vkp]) = lo | (hi << 16);
+    }
+  };
+
+  f32x16 o[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int ntiles = (L + ATT_BK - 1) / ATT_BK;
+  issue_k(0, 0);
+  load_v(0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  store_vt(0);
+  lds_barrier();
+
+  for (int j = 0; j < ntiles; ++j) {
+    const int buf = j & 1;
+    const bool more = j + 1 < ntiles;
+    if (more) {
+      issue_k(j + 1, buf ^ 1);
+      load_v(j + 1);
+    }
+    // ---- S^T = K Q^T for the 64 keys of tile j
+    const uint8_t* kb_lds = k_lds[buf];
+    f32x16 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+      const int row = 32 * kb + l32;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int c = 2 * st + h;
+        const uint4 kf = *reinterpret_cast<const uint4*>(kb_lds + row * 128 + ((c ^ fk(row)) * 16));
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf),
+                                                      __builtin_bit_cast(f16x8, qf[st]), s[kb], 0, 0, 0);
+      }
+    }
+    // ---- online softmax (scores scaled to log2 units)
+    const int key0 = j * ATT_BK;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
+        float x = s[kb][r] * scale_log2;
+        x = key < L ? x : -INFINITY;
+        s[kb][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    uint4 pf[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        f16x8 ph;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pv = __builtin_amdgcn_exp2f(s[kb][8 * p + e] - m_new);
+          psum += pv;
+          ph[e] = (_Float16)pv;
+        }
+        pf[2 * kb + p] = __builtin_bit_cast(uint4, ph);
+      }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    // ---- O^T += V^T P^T
+    const uint8_t* vt = vt_lds[buf];
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      const int d = 32 * db + l32;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int kb = st >> 1, p = st & 1;
+        const int kk = 32 * kb + 16 * p + 4 * h;
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vt + d * VT_PITCH + kk * 2);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vt + d * VT_PITCH + (kk + 8) * 2);
+        const uint4 vf = make_uint4(v0.x, v0.y, v1.x, v1.y);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
+                                                      __builtin_bit_cast(f16x8, pf[st]), o[db], 0, 0, 0);
+      }
+    }
+    if (more) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next K tile and V registers landed
+      store_vt(buf ^ 1);
+    }
+    lds_barrier();
+  }
+
+  // ---- normalise and store: lane (h, q) holds dims 32db + 8*(r/4) + 4h + r%4
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / l_tot;
+  if (qi < L) {
+    uint16_t* op = out + (tok0 + qi) * o_ts + (long)head * 64;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint2 w;
+        w.x = pack2<false>(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
+        w.y = pack2<false>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+        *reinterpret_cast<uint2*>(op + 32 * db + 8 * g + 4 * h) = w;
+      }
+  }
+}
+
+}  // namespace qv
+
+extern "C" int qv_attention_fwd(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t L,
+                                int64_t H, int64_t head_dim, int64_t q_token_stride, int64_t k_token_stride,
+                                int64_t v_token_stride, int64_t out_token_stride, float scale, void* stream) {
+  QV_CHECK_ARG(head_dim == 64, "only head_dim 64 is supported (got %lld)", (long long)head_dim);
+  QV_CHECK_ARG(B >= 0 && L >= 0 && H > 0, "bad shape B=%lld L=%lld H=%lld", (long long)B, (long long)L, (long long)H);
+  if (B == 0 || L == 0) return QV_OK;
+  QV_CHECK_ARG(q && k && v && out, "null pointer argument");
+  QV_CHECK_ARG(q_token_stride % 8 == 0 && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
+                   out_token_stride % 4 == 0 && q_token_stride >= H * 64 && k_token_stride >= H * 64 &&
+                   v_token_stride >= H * 64 && out_token_stride >= H * 64,
+               "token strides must cover the heads and keep 16-byte alignment");
+  QV_CHECK_ARG(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 &&
+                   ((uintptr_t)out % 8) == 0,
+               "q, k, v must be 16-byte and out 8-byte aligned");
+  QV_CHECK_ARG((uint64_t)L * k_token_stride * 2 < (1ull << 32) && (uint64_t)L * v_token_stride * 2 < (1ull << 32),
+               "sequence too long for 32-bit offsets");
+  const long qtiles = (L + qv::ATT_BQ - 1) / qv::ATT_BQ;
+  const long nwg = B * H * qtiles;
+  QV_CHECK_ARG(nwg <= INT32_MAX, "grid too large");
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(qv::attention_fwd_kernel, dim3((unsigned)nwg), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out, (int)L, (int)H,
+                     (long)q_token_stride, (long)k_token_stride, (long)v_token_stride, (long)out_token_stride,
+                     scale_log2);
+  return qv::check_launch("attention_fwd");
+}
