@@ -170,6 +170,18 @@ int qv_rope2d(const void* qkv, void* out, const int32_t* positions, const float*
               int64_t src_token_stride, int64_t dst_token_stride, int64_t dst_part_stride,
               void* stream);
 
+/*
+ * VGGT attention prologue fused in one pass, in place on a fp16 qkv buffer
+ * (T tokens x token_stride elements, [3][H][64] per token): per-head
+ * LayerNorm of q and k over the 64 head dims (q_gamma/q_beta, k_gamma/k_beta
+ * fp16 (64), eps), rounded to fp16, then the 2-D RoPE of qv_rope2d.  No
+ * counterpart in the reference extension (VGGT's qk-norm is in vggt-hf).
+ */
+int qv_qknorm_rope2d(void* qkv, const int32_t* positions, const float* cos_table,
+                     const float* sin_table, int64_t table_rows, const void* q_gamma,
+                     const void* q_beta, const void* k_gamma, const void* k_beta, float eps,
+                     int64_t T, int64_t H, int64_t token_stride, void* stream);
+
 /* ----------------------------------------------------------- attention */
 
 /*

@@ -80,3 +80,30 @@ def vggt_positions(S: int, grid: int = 37, specials: int = 5) -> np.ndarray:
     patch = np.stack([yy.ravel() + 1, xx.ravel() + 1], axis=1)
     frame = np.concatenate([np.zeros((specials, 2), np.int64), patch], axis=0)
     return np.tile(frame, (S, 1)).astype(np.int32)
+
+
+def _seq_sum_f32(v: np.ndarray) -> np.ndarray:
+    """Sum over the last axis strictly in index order, fp32."""
+    acc = np.zeros(v.shape[:-1], F32)
+    for i in range(v.shape[-1]):
+        acc = (acc + v[..., i]).astype(F32)
+    return acc
+
+
+def qknorm_rope2d(qk: np.ndarray, pos, cos_t, sin_t, qg, qb, kg, kb, eps: float = 1e-6) -> np.ndarray:
+    """VGGT attention prologue: per-head LayerNorm of q and k (affine over the
+    64 head dims, fp32 statistics summed in index order, two-pass variance),
+    rounded to fp16, then ``rope2d``.  qk: (T, 2, H, 64) fp16 -> same shape."""
+    x = np.asarray(qk).astype(F32)
+    mean = (_seq_sum_f32(x) / F32(64)).astype(F32)
+    d = (x - mean[..., None]).astype(F32)
+    var = (_seq_sum_f32((d * d).astype(F32)) / F32(64)).astype(F32)
+    rs = (F32(1.0) / np.sqrt((var + F32(eps)).astype(F32))).astype(F32)
+    g = np.stack([np.asarray(qg), np.asarray(kg)]).astype(F32)[None, :, None, :]
+    b = np.stack([np.asarray(qb), np.asarray(kb)]).astype(F32)[None, :, None, :]
+    t = ((d * rs[..., None]).astype(F32) * g).astype(F32)
+    t = (t + b).astype(F32).astype(np.float16)
+    out = np.empty_like(t)
+    for part in range(2):
+        out[:, part] = rope2d(t[:, part], pos, cos_t, sin_t)
+    return out

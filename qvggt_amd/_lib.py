@@ -41,6 +41,7 @@ SIGNATURES: dict[str, list] = {
     "qv_layernorm": [_vp, _vp, _vp, _vp, _f32, _i64, _i64, _i32, _vp],
     "qv_rope_with_pos": [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
     "qv_rope2d": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp],
+    "qv_qknorm_rope2d": [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _f32, _i64, _i64, _i64, _vp],
     "qv_attention_fwd": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp],
 }
 _RESTYPES = {"qv_last_error": C.c_char_p, "qv_version": C.c_char_p}

@@ -506,3 +506,25 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_len: int, s
         _lib.call("qv_attention_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(out), T // seq_len, seq_len, H, 64,
                   q.stride(0), k.stride(0), v.stride(0), out.stride(0), C.c_float(scale), _stream(dev))
     return out
+
+
+def qknorm_rope2d(qkv: torch.Tensor, positions: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+                  heads: int, q_gamma: torch.Tensor, q_beta: torch.Tensor, k_gamma: torch.Tensor,
+                  k_beta: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """In place on qkv (T, 3*heads*64) fp16: per-head LayerNorm of q and k, then
+    VGGT 2-D RoPE (see ``rope2d``).  Returns qkv."""
+    what = "qknorm_rope2d"
+    if qkv.dtype != torch.float16 or qkv.shape[-1] != 3 * heads * 64 or not qkv.is_contiguous():
+        _fail(f"{what}: qkv must be contiguous float16 (T, 3*heads*64)")
+    T = qkv.numel() // qkv.shape[-1]
+    for name, t in (("q_gamma", q_gamma), ("q_beta", q_beta), ("k_gamma", k_gamma), ("k_beta", k_beta)):
+        if t.dtype != torch.float16 or t.numel() != 64:
+            _fail(f"{what}: {name} must be float16 (64,)")
+    if positions.dtype != torch.int32 or positions.numel() != 2 * T:
+        _fail(f"{what}: positions must be int32 (T, 2)")
+    dev = _on_gpu(qkv, positions, cos_table, sin_table, q_gamma, q_beta, k_gamma, k_beta, what=what)
+    with _device(dev):
+        _lib.call("qv_qknorm_rope2d", _ptr(qkv), _ptr(_contig(positions)), _ptr(cos_table), _ptr(sin_table),
+                  cos_table.shape[0], _ptr(_contig(q_gamma)), _ptr(_contig(q_beta)), _ptr(_contig(k_gamma)),
+                  _ptr(_contig(k_beta)), C.c_float(eps), T, heads, 3 * heads * 64, _stream(dev))
+    return qkv

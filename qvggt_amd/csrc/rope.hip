@@ -105,9 +105,85 @@ __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict_
   *reinterpret_cast<uint4*>(d + 16) = __builtin_bit_cast(uint4, ob);
 }
 
+// VGGT attention prologue, fused: per-head LayerNorm of q and k (qk-norm,
+// affine, over the 64 head dims), rounded to fp16, then the 2-D RoPE above,
+// in place in the fused qkv buffer.  One thread per (token, part, head) row of
+// 64 values; statistics in fp32 with the row summed in index order, two-pass
+// variance; one rounding per fp32 operation.
+__global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
+    uint16_t* __restrict__ qkv, const int* __restrict__ pos, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int P, const uint16_t* __restrict__ qg, const uint16_t* __restrict__ qb,
+    const uint16_t* __restrict__ kg, const uint16_t* __restrict__ kb, float eps, int T, int H, long tok_stride) {
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (long)T * 2 * H) return;
+  const int tok = (int)(gid / (2 * H));
+  const int r = (int)(gid % (2 * H));
+  const int part = r / H, head = r % H;
+  uint16_t* row = qkv + (size_t)tok * tok_stride + (size_t)part * H * 64 + (size_t)head * 64;
+  float x[64];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const f16x8 v = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(row)[c]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[8 * c + e] = (float)v[e];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) s = s + x[i];
+  const float mean = s / 64.0f;
+  float s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    x[i] = x[i] - mean;
+    s2 = s2 + x[i] * x[i];
+  }
+  const float rs = 1.0f / __builtin_sqrtf(s2 / 64.0f + eps);
+  const uint16_t* g = part ? kg : qg;
+  const uint16_t* b = part ? kb : qb;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const float t = (x[i] * rs) * to_f32(g[i], false) + to_f32(b[i], false);
+    x[i] = (float)__builtin_bit_cast(_Float16, from_f32<false>(t));   // q_norm output is fp16
+  }
+  f16x8 o[8];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    int p = pos[2 * tok + half];
+    p = p < 0 ? 0 : (p >= P ? P - 1 : p);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float c = cos_t[p * 16 + i], sn = sin_t[p * 16 + i];
+      const float a = x[32 * half + i], bb = x[32 * half + 16 + i];
+      const int d0 = 32 * half + i, d1 = d0 + 16;
+      o[d0 >> 3][d0 & 7] = __builtin_bit_cast(_Float16, from_f32<false>(a * c - bb * sn));
+      o[d1 >> 3][d1 & 7] = __builtin_bit_cast(_Float16, from_f32<false>(bb * c + a * sn));
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) reinterpret_cast<uint4*>(row)[c] = __builtin_bit_cast(uint4, o[c]);
+}
+
 }  // namespace qv
 
 using namespace qv;
+
+extern "C" int qv_qknorm_rope2d(void* qkv, const int32_t* positions, const float* cos_table, const float* sin_table,
+                                int64_t table_rows, const void* q_gamma, const void* q_beta, const void* k_gamma,
+                                const void* k_beta, float eps, int64_t T, int64_t H, int64_t token_stride,
+                                void* stream) {
+  QV_CHECK_ARG(T >= 0 && H > 0 && table_rows > 0 && table_rows <= INT32_MAX, "bad shape");
+  if (T == 0) return QV_OK;
+  QV_CHECK_ARG(qkv && positions && cos_table && sin_table && q_gamma && q_beta && k_gamma && k_beta,
+               "null pointer argument");
+  QV_CHECK_ARG(token_stride % 8 == 0 && token_stride >= 2 * H * 64 && ((uintptr_t)qkv % 16) == 0,
+               "qkv rows must be 16-byte aligned and hold q and k");
+  const long total = T * 2 * H;
+  hipLaunchKernelGGL(qknorm_rope2d_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (uint16_t*)qkv, positions, cos_table, sin_table, (int)table_rows, (const uint16_t*)q_gamma,
+                     (const uint16_t*)q_beta, (const uint16_t*)k_gamma, (const uint16_t*)k_beta, eps, (int)T, (int)H,
+                     (long)token_stride);
+  return check_launch("qknorm_rope2d");
+}
 
 extern "C" int qv_rope_with_pos(const void* x, const float* freqs, void* out, int dtype, int64_t S, int64_t B,
                                 int64_t H, int64_t D, int64_t D2, const int64_t* x_strides,

@@ -188,3 +188,24 @@ def test_rope2d_bit_exact(gpu, inplace):
     for part in range(2):
         ref = R.rope2d(x[:, part], pos, c, s)
         assert np.array_equal(got[:, part].view(np.int16), ref.view(np.int16))
+
+
+def test_qknorm_rope2d_bit_exact(gpu):
+    from qvggt_amd import awq_inference_engine as E
+    S, H = 2, 16
+    pos = R.vggt_positions(S)
+    T = pos.shape[0]
+    rng = _rng(11)
+    qkv = (rng.standard_normal((T, 3 * H * 64)) * 2 + 0.3).astype(np.float16)
+    qg, qb, kg, kb = ((1 + 0.1 * rng.standard_normal(64)).astype(np.float16) if i % 2 == 0
+                      else (0.1 * rng.standard_normal(64)).astype(np.float16) for i in range(4))
+    c, s = R.rope2d_tables(38)
+    ct, st = E.rope2d_tables(38, device=gpu)
+    qt = torch.from_numpy(qkv.copy()).to(gpu)
+    E.qknorm_rope2d(qt, torch.from_numpy(pos).to(gpu), ct, st, H,
+                    *[torch.from_numpy(v).to(gpu) for v in (qg, qb, kg, kb)], eps=1e-6)
+    got = qt.view(T, 3, H, 64).cpu().numpy()
+    x = qkv.reshape(T, 3, H, 64)
+    ref = R.qknorm_rope2d(x[:, :2], pos, c, s, qg, qb, kg, kb, 1e-6)
+    assert np.array_equal(got[:, :2].view(np.int16), ref.view(np.int16))
+    assert np.array_equal(got[:, 2], x[:, 2])
