@@ -98,6 +98,23 @@ __device__ __forceinline__ size_t qw_chunk_u32(int n, int kt, int g, int K) {
          (g & 1) * 4;
 }
 
+// Bias / GELU on four consecutive channels n..n+3 (fp32, before the single
+// rounding to the 16-bit output type).
+template <bool BF16, int EPI>
+__device__ __forceinline__ void epilogue_apply4(const uint16_t* __restrict__ bias, float (&r)[4], int n) {
+  if constexpr (EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU) {
+    const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
+    r[0] += to_f32((uint16_t)(b.x & 0xFFFF), BF16);
+    r[1] += to_f32((uint16_t)(b.x >> 16), BF16);
+    r[2] += to_f32((uint16_t)(b.y & 0xFFFF), BF16);
+    r[3] += to_f32((uint16_t)(b.y >> 16), BF16);
+  }
+  if constexpr (EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_GELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = gelu_erf(r[i]);
+  }
+}
+
 // Bias / GELU epilogue on four consecutive channels n..n+3 of token m, one
 // rounding to the 16-bit output type, one 8-byte store.
 template <bool BF16, int EPI>

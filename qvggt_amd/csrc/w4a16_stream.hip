@@ -20,6 +20,8 @@
 // operands (activations: 8 contiguous halves of chunk 4h + s).  Output: lane
 // (h, l), register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the tile.
 // LDS per workgroup: 3 x (BM*128 + 9 KB); BM = 128 -> 75 KB, 2 workgroups/CU.
+// The epilogue reuses that LDS to stage each wave's BM x 64 output tile and
+// writes it back as whole 128-byte rows.
 #include "w4a16_common.h"
 
 namespace qv {
@@ -149,20 +151,39 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
     compute(ks % NSTAGE);
   }
 
+  // ---- epilogue: the wave's BM x 64 output tile goes through LDS so that the
+  // global stores are whole 128-byte rows (direct 8-byte stores from the MFMA
+  // layout cost ~3x the output size in HBM write traffic).
+  lds_barrier();  // every wave is done reading the pipeline stages
+  constexpr int EP = 144;  // bytes per staged row: 64 fp16 + 16 B pad
+  static_assert(4 * BM * EP <= NSTAGE * STAGE, "epilogue staging fits in the pipeline LDS");
+  uint8_t* stg = lds + wave * (BM * EP);
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int n = n0 + 64 * wave + 32 * j + 8 * q + 4 * h;
-      if (n >= N) continue;
+      const int nl = 32 * j + 8 * q + 4 * h;
+      const int n = n0 + 64 * wave + nl;
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        const int m = m0 + 32 * i + l32;
-        if (m < M)
-          epilogue_store4<BF16, EPI>(out, bias, acc[j][i][4 * q], acc[j][i][4 * q + 1],
-                                     acc[j][i][4 * q + 2], acc[j][i][4 * q + 3], m, n, N);
+        float r[4] = {acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
+        epilogue_apply4<BF16, EPI>(bias, r, n < N ? n : 0);
+        uint2 o;
+        o.x = pack2<BF16>(r[0], r[1]);
+        o.y = pack2<BF16>(r[2], r[3]);
+        *reinterpret_cast<uint2*>(stg + (32 * i + l32) * EP + nl * 2) = o;
       }
     }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int it = 0; it < BM * 8 / 64; ++it) {
+    const int idx = it * 64 + lane;
+    const int row = idx >> 3, c = idx & 7;
+    const int m = m0 + row, n = n0 + 64 * wave + 8 * c;
+    if (m < M && n < N)
+      *reinterpret_cast<uint4*>(out + (size_t)m * N + n) = *reinterpret_cast<const uint4*>(stg + row * EP + c * 16);
   }
 }
 

@@ -114,14 +114,42 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
     compute(ks % NSTAGE);
   }
 
+  if constexpr (OUT == 2) {
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
+    for (int j = 0; j < NT; ++j) {
 #pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int n = n0 + 64 * wave + 32 * j + 8 * qd + 4 * h;
-      if (n >= N) continue;
-      float wsn[4], bn[4] = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (OUT != 2) {
+      for (int qd = 0; qd < 4; ++qd) {
+        const int n = n0 + 64 * wave + 32 * j + 8 * qd + 4 * h;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const int m = m0 + 32 * i + l32;
+          if (m >= M) continue;
+          int4 o = make_int4(acc[j][i][4 * qd], acc[j][i][4 * qd + 1], acc[j][i][4 * qd + 2], acc[j][i][4 * qd + 3]);
+          *reinterpret_cast<int4*>(reinterpret_cast<int32_t*>(out) + (size_t)m * N + n) = o;
+        }
+      }
+    }
+  } else {
+    // fp16 output: the wave's BM x 64 tile is staged in LDS (reusing the
+    // pipeline buffers) and written back as whole 128-byte rows.
+    lds_barrier();  // every wave is done reading the pipeline stages
+    constexpr int EP = 144;  // bytes per staged row: 64 fp16 + 16 B pad
+    static_assert(4 * BM * EP <= NSTAGE * STAGE, "epilogue staging fits in the pipeline LDS");
+    uint8_t* stg = lds + wave * (BM * EP);
+    float am[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int m = m0 + 32 * i + l32;
+      am[i] = to_f32(as[m < M ? m : M - 1], false);
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int nl = 32 * j + 8 * qd + 4 * h;
+        const int n = min(n0 + 64 * wave + nl, N - 4);
+        float wsn[4], bn[4] = {0.f, 0.f, 0.f, 0.f};
         const uint2 wv = *reinterpret_cast<const uint2*>(ws + n);
         wsn[0] = to_f32((uint16_t)(wv.x & 0xFFFF), false);
         wsn[1] = to_f32((uint16_t)(wv.x >> 16), false);
@@ -134,21 +162,13 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
           bn[2] = to_f32((uint16_t)(bv.y & 0xFFFF), false);
           bn[3] = to_f32((uint16_t)(bv.y >> 16), false);
         }
-      }
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const int m = m0 + 32 * i + l32;
-        if (m >= M) continue;
-        if constexpr (OUT == 2) {
-          int4 o = make_int4(acc[j][i][4 * qd], acc[j][i][4 * qd + 1], acc[j][i][4 * qd + 2], acc[j][i][4 * qd + 3]);
-          *reinterpret_cast<int4*>(reinterpret_cast<int32_t*>(out) + (size_t)m * N + n) = o;
-        } else {
-          const float am = to_f32(as[m], false);
+        for (int i = 0; i < MT; ++i) {
           float r[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float t = (float)acc[j][i][4 * qd + e] * wsn[e];
-            t = t * am;
+            t = t * am[i];
             if constexpr (OUT == 1) t = t + bn[e];
             // keep the fp32 rounding of t: without this the backend fuses the last
             // multiply and the fp16 conversion into one v_fma_mixlo_f16 (one rounding)
@@ -158,9 +178,20 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
           uint2 o;
           o.x = pack2<false>(r[0], r[1]);
           o.y = pack2<false>(r[2], r[3]);
-          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + (size_t)m * N + n) = o;
+          *reinterpret_cast<uint2*>(stg + (32 * i + l32) * EP + nl * 2) = o;
         }
       }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+    __builtin_amdgcn_wave_barrier();
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(out);
+#pragma unroll
+    for (int it = 0; it < BM * 8 / 64; ++it) {
+      const int idx = it * 64 + lane;
+      const int row = idx >> 3, c = idx & 7;
+      const int m = m0 + row, n = n0 + 64 * wave + 8 * c;
+      if (m < M && n < N)
+        *reinterpret_cast<uint4*>(o16 + (size_t)m * N + n) = *reinterpret_cast<const uint4*>(stg + row * EP + c * 16);
     }
   }
 }

@@ -1,0 +1,92 @@
+"""Fixed workloads for rocprofv3 runs (kernel traces and PMC counters).
+
+    python qvggt_amd/profiling.py copy                 # traffic calibration
+    python qvggt_amd/profiling.py gemm M K N [--gelu] [--reps R]
+    python qvggt_amd/profiling.py aggregator [--frames S] [--w8a8]
+
+``copy`` launches one elementwise kernel that reads 512 MiB and writes
+512 MiB, three times: the FETCH_SIZE / WRITE_SIZE it reports per dispatch
+calibrate those counters against known byte counts.  ``gemm`` runs the W4A16
+linear (optionally with the fused bias + GELU epilogue) on seeded synthetic
+data; ``aggregator`` runs the VGGT aggregator forward twice (the first call
+warms up).  Every mode prints one line when done.
+"""
+from __future__ import annotations
+
+import argparse
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+
+
+def _copy():
+    import torch
+    a = torch.randn(256 * 1024 * 1024, dtype=torch.float16, device="cuda")  # 512 MiB
+    b = torch.empty_like(a)
+    for _ in range(3):
+        torch.mul(a, 1.0, out=b)
+    torch.cuda.synchronize()
+    print("copy: 3 launches, each 512 MiB read + 512 MiB written", flush=True)
+
+
+def _gemm(M, K, N, gelu, reps):
+    import torch
+
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd._lib import QV_EPI_BIAS_GELU, QV_EPI_NONE
+    from qvggt_amd.awq.qmodule import calculate_zeros_width
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(M, K, generator=g).half().to(dev)
+    qw = torch.randint(-32768, 32768, (N // 4, K), generator=g, dtype=torch.int32).to(torch.int16).to(dev)
+    rows = calculate_zeros_width(K, 128) * 8
+    s = (torch.rand(rows, N, generator=g) * 0.015 + 0.005).half().to(dev)
+    z = (-(s.float() * torch.randint(0, 16, (rows, N), generator=g).float().to(dev))).half()
+    b = torch.zeros(N, dtype=torch.float16, device=dev)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    for _ in range(reps):
+        E.w4a16_linear(x, qw, s, z, bias=b, epilogue=QV_EPI_BIAS_GELU if gelu else QV_EPI_NONE, out=out)
+    torch.cuda.synchronize()
+    print(f"gemm: M={M} K={K} N={N} gelu={gelu}, {reps} launches", flush=True)
+
+
+def _aggregator(S, w8a8):
+    import torch
+
+    from qvggt_amd import aggregator as AG
+
+    dev = torch.device("cuda:0")
+    agg = AG.Aggregator.random(w8a8=w8a8, seed=0, device=dev)
+    img = torch.rand(S, 3, AG.IMG, AG.IMG, generator=torch.Generator().manual_seed(1)).half().to(dev)
+    for _ in range(2):
+        agg(img)
+        torch.cuda.synchronize()
+    print(f"aggregator: S={S} w8a8={w8a8}, 2 forwards", flush=True)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="mode", required=True)
+    sub.add_parser("copy")
+    g = sub.add_parser("gemm")
+    g.add_argument("M", type=int)
+    g.add_argument("K", type=int)
+    g.add_argument("N", type=int)
+    g.add_argument("--gelu", action="store_true")
+    g.add_argument("--reps", type=int, default=3)
+    a = sub.add_parser("aggregator")
+    a.add_argument("--frames", type=int, default=32)
+    a.add_argument("--w8a8", action="store_true")
+    args = ap.parse_args(argv)
+    if args.mode == "copy":
+        _copy()
+    elif args.mode == "gemm":
+        _gemm(args.M, args.K, args.N, args.gelu, args.reps)
+    else:
+        _aggregator(args.frames, args.w8a8)
+
+
+if __name__ == "__main__":
+    main()

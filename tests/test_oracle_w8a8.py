@@ -180,3 +180,29 @@ def test_rope2d_is_two_1d_ropes_and_specials_unrotated():
         ref = R.rope_with_pos(sub.astype(np.float32), fr[None].transpose(0, 1, 2).reshape(1, T, 32))
         assert np.abs(ref[:, 0].astype(np.float64) - y[:, :, 32 * half:32 * half + 32]).max() < 2e-3
     assert pos.shape == (42, 2) and pos[:6].sum() == 0 and pos[6:].min() == 1
+
+
+def test_qknorm_rope2d_is_float64_layernorm_then_complex_rotation():
+    """Independent restatement: float64 per-head LayerNorm, then each 2-D RoPE
+    half as a complex rotation by p * base**(-i/16) (base 100)."""
+    rng = np.random.default_rng(9)
+    T, H = 41, 2
+    qk = (rng.standard_normal((T, 2, H, 64)) * 3 + 0.5).astype(np.float16)
+    g = [(1 + 0.1 * rng.standard_normal(64)).astype(np.float16) for _ in range(2)]
+    b = [(0.1 * rng.standard_normal(64)).astype(np.float16) for _ in range(2)]
+    pos = R.vggt_positions(1, grid=6, specials=5)
+    c, s = R.rope2d_tables(8)
+    y = R.qknorm_rope2d(qk, pos, c, s, g[0], b[0], g[1], b[1]).astype(np.float64)
+    x = qk.astype(np.float64)
+    ln = (x - x.mean(-1, keepdims=True)) / np.sqrt(x.var(-1, keepdims=True) + 1e-6)
+    ln = ln * np.stack(g).astype(np.float64)[None, :, None] + np.stack(b).astype(np.float64)[None, :, None]
+    freq = 100.0 ** (-np.arange(16) / 16.0)
+    for half in range(2):
+        th = pos[:, half].astype(np.float64)[:, None] * freq[None]          # (T, 16)
+        z = ln[..., 32 * half:32 * half + 16] + 1j * ln[..., 32 * half + 16:32 * half + 32]
+        r = z * np.exp(1j * th)[:, None, None, :]
+        tol = 2e-3 * np.abs(ln).max()
+        assert np.abs(y[..., 32 * half:32 * half + 16] - r.real).max() < tol
+        assert np.abs(y[..., 32 * half + 16:32 * half + 32] - r.imag).max() < tol
+    # specials (position 0) are the bare fp16 LayerNorm
+    assert np.abs(y[:5] - ln[:5]).max() < 2e-3 * np.abs(ln).max()
