@@ -244,8 +244,10 @@ def profiled_traffic():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--prewarm-s", type=float, default=1.0,
+                    help="seconds of untimed steps before the warm-up steps (clock ramp)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-aggregator", action="store_true")
     ap.add_argument("--no-kernel-suite", action="store_true")
@@ -282,6 +284,13 @@ def main():
         if evs is not None:
             evs[2].record(stream)
 
+    # Untimed: first bring the GPU to its sustained clock (an idle MI355X takes
+    # a few hundred ms of load to get there), then the W warm-up steps.
+    t_end = time.perf_counter() + args.prewarm_s
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()

@@ -104,6 +104,21 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
   }
   const int fa = (l32 & 7) ^ ((l32 >> 3) & 1);  // fA(32*i + l32) is the same for all i
 
+  auto dq = [&](int s, const uint4 (&wq)[NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT], uint4 (&wf)[NT]) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      switch (s) {
+        case 0: wf[j] = dq_frag<BF16, 0>(wq[j], sv[j], zv[j]); break;
+        case 1: wf[j] = dq_frag<BF16, 1>(wq[j], sv[j], zv[j]); break;
+        case 2: wf[j] = dq_frag<BF16, 2>(wq[j], sv[j], zv[j]); break;
+        default: wf[j] = dq_frag<BF16, 3>(wq[j], sv[j], zv[j]); break;
+      }
+    }
+  };
+  // One stage: k-step s issues the LDS reads of step s+1's activations, then
+  // its own MFMAs, then dequantises step s+1's weights (VALU that co-issues
+  // with the MFMAs in flight).  The scheduling fences keep the compiler from
+  // sinking the reads next to their use, which would expose LDS latency.
   auto compute = [&](int st) {
     const uint8_t* base = lds + st * STAGE;
     uint4 wq[NT];
@@ -114,25 +129,27 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
       sv[j] = *reinterpret_cast<const uint16_t*>(base + s_off[j]);
       zv[j] = *reinterpret_cast<const uint16_t*>(base + s_off[j] + S_BYTES);
     }
+    uint4 af[2][MT], wf[2][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      af[0][i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 128 + (uint32_t)(((4 * h) ^ fa) * 16));
+    dq(0, wq, sv, zv, wf[0]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      uint4 wf[NT];
+      if (s < 3) {
+        const uint32_t col = (uint32_t)(((4 * h + s + 1) ^ fa) * 16);
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        switch (s) {
-          case 0: wf[j] = dq_frag<BF16, 0>(wq[j], sv[j], zv[j]); break;
-          case 1: wf[j] = dq_frag<BF16, 1>(wq[j], sv[j], zv[j]); break;
-          case 2: wf[j] = dq_frag<BF16, 2>(wq[j], sv[j], zv[j]); break;
-          default: wf[j] = dq_frag<BF16, 3>(wq[j], sv[j], zv[j]); break;
-        }
+        for (int i = 0; i < MT; ++i)
+          af[(s + 1) & 1][i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 128 + col);
       }
-      const uint32_t col = (uint32_t)(((4 * h + s) ^ fa) * 16);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        const uint4 af = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 128 + col);
 #pragma unroll
-        for (int j = 0; j < NT; ++j) acc[j][i] = mfma32<BF16>(wf[j], af, acc[j][i]);
+        for (int j = 0; j < NT; ++j) acc[j][i] = mfma32<BF16>(wf[s & 1][j], af[s & 1][i], acc[j][i]);
       }
+      if (s < 3) dq(s + 1, wq, sv, zv, wf[(s + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 

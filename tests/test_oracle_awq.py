@@ -258,3 +258,34 @@ def test_gemm_ref_brute_force_and_special_cases():
 def test_rel_err_metric():
     assert O.rel_err(np.array([1.0, 2.0]), np.array([1.0, 2.0])) == 0
     assert abs(O.rel_err(np.array([1.0, 2.1]), np.array([1.0, 2.0])) - 0.05) < 1e-12
+
+
+# The W4A16 epilogue's GELU: max(v,0) - |v| * 2^P(min(|v|,6)), P the degree-9
+# fit of log2 Phi(-a) used by gelu_erf in qvggt_amd/csrc/common.h.
+GELU_P = [4.286207300e-08, -1.151150400e-06, 1.097847053e-05, -1.475488898e-05, -6.680788938e-04,
+          7.986173965e-03, -5.339243263e-02, -4.587580562e-01, -1.151201010e+00, -9.999949932e-01]
+
+
+def _gelu_poly_f32(v):
+    v = np.asarray(v, np.float32)
+    a = np.abs(v)
+    t = np.minimum(a, np.float32(6.0))
+    p = np.full_like(t, np.float32(GELU_P[0]))
+    for c in GELU_P[1:]:
+        p = (p.astype(np.float64) * t + np.float32(c)).astype(np.float32)   # fma: one rounding
+    e = np.exp2(p.astype(np.float64)).astype(np.float32)
+    return (np.maximum(v, 0).astype(np.float64) - a.astype(np.float64) * e).astype(np.float32)
+
+
+def test_gelu_polynomial_matches_erf_gelu():
+    """The kernel's GELU (emulated in float32) against the float64 erf form:
+    |error| <= 3e-7 over [-30, 30], exact zero / identity far out."""
+    from scipy.special import erf
+    v = np.linspace(-30, 30, 600001).astype(np.float32)
+    v64 = v.astype(np.float64)
+    ref = 0.5 * v64 * (1 + erf(v64 / np.sqrt(2)))
+    got = _gelu_poly_f32(v).astype(np.float64)
+    assert np.abs(got - ref).max() <= 3e-7
+    assert _gelu_poly_f32(np.float32(0.0)) == 0.0
+    assert _gelu_poly_f32(np.float32(25.0)) == np.float32(25.0)
+    assert abs(_gelu_poly_f32(np.float32(-25.0))) < 1e-7
