@@ -8,7 +8,12 @@
 //
 // Workgroup: 4 waves, 32 queries each (128 queries of one (sequence, head)).
 // Per 64-key tile a wave computes S^T = K Q^T (2 x 4 v_mfma_f32_32x32x16_f16),
-// the online softmax in registers, and O^T += V^T P^T (2 x 4 more MFMAs):
+// the online softmax in registers, and O^T += V^T P^T (2 x 4 more MFMAs).
+// The softmax is trimmed to what the MFMAs cannot hide: key masking only on
+// the last (partial) tile, one fma + exp2 per score, row sums by v_dot2 on
+// the fp16 P values, and a lazy rescale -- the reference maximum moves only
+// when a tile exceeds it by 2^8, so most tiles skip the O *= alpha pass.
+// Layouts:
 //  * S^T layout: lane (h = lane/32, q = lane%32) holds, for key block kb,
 //    keys 32kb + 8*(r/4) + 4h + r%4 (r = 0..15) of query q.  A query's 64
 //    scores are split between lanes q and q+32: one cross-lane exchange per
@@ -28,9 +33,33 @@ constexpr int ATT_BQ = 128;   // queries per workgroup
 constexpr int ATT_BK = 64;    // keys per tile
 constexpr int VT_PITCH = 136; // bytes per V^T row (64 keys + 8 B pad)
 
+constexpr float RESCALE_SLACK = 8.0f;  // log2 units: P <= 256 between rescales
+
 __device__ __forceinline__ int fk(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-__global__ __launch_bounds__(256) void attention_fwd_kernel(
+// max / sum of x over lanes l and l ^ 32.  v_permlane32_swap exchanges the
+// upper half of its first operand with the lower half of its second; with
+// both holding x, lane l ends with {x[l & 31], x[(l & 31) + 32]} in the pair.
+// Written as inline asm: the compiler's model of the builtin folds the two
+// results into one when both operands carry the same value.  The s_nop
+// covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void half_pair(float x, float& a, float& b) {
+  a = x;
+  b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float half_max(float x) {
+  float a, b;
+  half_pair(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float half_sum(float x) {
+  float a, b;
+  half_pair(x, a, b);
+  return a + b;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attention_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ out, int L, int H, long q_ts, long kv_ts, long v_ts, long o_ts, float scale_log2) {
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][ATT_BK * 128];
@@ -96,80 +125,85 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(
     }
   };
 
+  const int ntiles = (L + ATT_BK - 1) / ATT_BK;
   f32x16 o[2];
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  // m_use: the running reference maximum in log2 units.  It is only raised
+  // when a tile's maximum exceeds it by more than RESCALE_SLACK, so P values
+  // stay <= 2^RESCALE_SLACK and most tiles skip the O rescale.
+  float m_use = -INFINITY, l_run = 0.f;
+  const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-  const int ntiles = (L + ATT_BK - 1) / ATT_BK;
-  issue_k(0, 0);
-  load_v(0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  store_vt(0);
-  lds_barrier();
-
-  for (int j = 0; j < ntiles; ++j) {
+  auto tile = [&](int j, bool mask) {
     const int buf = j & 1;
     const bool more = j + 1 < ntiles;
     if (more) {
       issue_k(j + 1, buf ^ 1);
       load_v(j + 1);
     }
-    // ---- S^T = K Q^T for the 64 keys of tile j
+    // ---- S^T = K Q^T for the 64 keys of tile j (raw dot products)
     const uint8_t* kb_lds = k_lds[buf];
-    f32x16 s[2];
+    f32x16 sc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
       const int row = 32 * kb + l32;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int c = 2 * st + h;
         const uint4 kf = *reinterpret_cast<const uint4*>(kb_lds + row * 128 + ((c ^ fk(row)) * 16));
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf),
-                                                      __builtin_bit_cast(f16x8, qf[st]), s[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf),
+                                                       __builtin_bit_cast(f16x8, qf[st]),
+                                                       st == 0 ? f32x16{} : sc[kb], 0, 0, 0);
       }
     }
-    // ---- online softmax (scores scaled to log2 units)
-    const int key0 = j * ATT_BK;
-    float mx = -INFINITY;
+    if (mask) {
+      const int key0 = j * ATT_BK + 4 * h;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = key0 + 32 * kb + 8 * (r >> 2) + 4 * h + (r & 3);
-        float x = s[kb][r] * scale_log2;
-        x = key < L ? x : -INFINITY;
-        s[kb][r] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    float psum = 0.f;
+        for (int r = 0; r < 16; ++r)
+          if (key0 + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[kb][r] = -INFINITY;
+    }
+    // ---- tile maximum of this query (both lane halves hold 32 keys each)
+    float mx = sc[0][0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[0][r]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][r]);
+    mx = half_max(mx) * scale_log2;
+    // ---- lazy rescale: wave-uniform branch, taken when any query's tile
+    // maximum exceeds its reference by more than the slack
+    const bool need = mx > m_use + RESCALE_SLACK;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float m_new = need ? mx : m_use;
+      const float alpha = __builtin_amdgcn_exp2f(m_use - m_new);  // 0 on the first tile, 1 if !need
+      m_use = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    }
+    // ---- P = 2^(s * scale_log2 - m_use) in fp16, row sums from the fp16 values
     uint4 pf[4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        f16x8 ph;
+      for (int pp = 0; pp < 2; ++pp) {
+        uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pv = __builtin_amdgcn_exp2f(s[kb][8 * p + e] - m_new);
-          psum += pv;
-          ph[e] = (_Float16)pv;
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * pp + 2 * e], scale_log2, -m_use));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * pp + 2 * e + 1], scale_log2, -m_use));
+          const f16x2 ph = {(_Float16)p0, (_Float16)p1};
+          l_run = __builtin_amdgcn_fdot2(ph, ones, l_run, false);
+          w[e] = __builtin_bit_cast(uint32_t, ph);
         }
-        pf[2 * kb + p] = __builtin_bit_cast(uint4, ph);
+        pf[2 * kb + pp] = make_uint4(w[0], w[1], w[2], w[3]);
       }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
     // ---- O^T += V^T P^T
     const uint8_t* vt = vt_lds[buf];
 #pragma unroll
@@ -177,8 +211,8 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(
       const int d = 32 * db + l32;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const int kb = st >> 1, p = st & 1;
-        const int kk = 32 * kb + 16 * p + 4 * h;
+        const int kb = st >> 1, pp = st & 1;
+        const int kk = 32 * kb + 16 * pp + 4 * h;
         const uint2 v0 = *reinterpret_cast<const uint2*>(vt + d * VT_PITCH + kk * 2);
         const uint2 v1 = *reinterpret_cast<const uint2*>(vt + d * VT_PITCH + (kk + 8) * 2);
         const uint4 vf = make_uint4(v0.x, v0.y, v1.x, v1.y);
@@ -191,10 +225,19 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(
       store_vt(buf ^ 1);
     }
     lds_barrier();
-  }
+  };
+
+  issue_k(0, 0);
+  load_v(0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  store_vt(0);
+  lds_barrier();
+  const int nfull = L / ATT_BK;        // tiles with every key valid
+  for (int j = 0; j < nfull; ++j) tile(j, false);
+  if (nfull < ntiles) tile(nfull, true);
 
   // ---- normalise and store: lane (h, q) holds dims 32db + 8*(r/4) + 4h + r%4
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = half_sum(l_run);
   const float inv = 1.0f / l_tot;
   if (qi < L) {
     uint16_t* op = out + (tok0 + qi) * o_ts + (long)head * 64;
