@@ -82,22 +82,29 @@ def vggt_positions(S: int, grid: int = 37, specials: int = 5) -> np.ndarray:
     return np.tile(frame, (S, 1)).astype(np.int32)
 
 
-def _seq_sum_f32(v: np.ndarray) -> np.ndarray:
-    """Sum over the last axis strictly in index order, fp32."""
-    acc = np.zeros(v.shape[:-1], F32)
-    for i in range(v.shape[-1]):
-        acc = (acc + v[..., i]).astype(F32)
-    return acc
+def _lane8_sum_f32(v: np.ndarray) -> np.ndarray:
+    """fp32 sum over the last axis (64) in the kernel's order: lane j (0..7)
+    sums elements 8j..8j+7 in index order, then a butterfly over lanes j ^ 1,
+    j ^ 2, j ^ 4 (pairwise adds; every lane ends with the same value)."""
+    v = np.asarray(v, F32).reshape(np.shape(v)[:-1] + (8, 8))     # [..., lane j, element e]
+    lanes = np.zeros(v.shape[:-1], F32)
+    for e in range(8):
+        lanes = (lanes + v[..., e]).astype(F32)
+    idx = np.arange(8)
+    for off in (1, 2, 4):
+        lanes = (lanes + lanes[..., idx ^ off]).astype(F32)
+    return lanes[..., 0]
 
 
 def qknorm_rope2d(qk: np.ndarray, pos, cos_t, sin_t, qg, qb, kg, kb, eps: float = 1e-6) -> np.ndarray:
     """VGGT attention prologue: per-head LayerNorm of q and k (affine over the
-    64 head dims, fp32 statistics summed in index order, two-pass variance),
+    64 head dims, fp32 statistics summed in the kernel's 8-lane order
+    (``_lane8_sum_f32``), two-pass variance),
     rounded to fp16, then ``rope2d``.  qk: (T, 2, H, 64) fp16 -> same shape."""
     x = np.asarray(qk).astype(F32)
-    mean = (_seq_sum_f32(x) / F32(64)).astype(F32)
+    mean = (_lane8_sum_f32(x) / F32(64)).astype(F32)
     d = (x - mean[..., None]).astype(F32)
-    var = (_seq_sum_f32((d * d).astype(F32)) / F32(64)).astype(F32)
+    var = (_lane8_sum_f32((d * d).astype(F32)) / F32(64)).astype(F32)
     rs = (F32(1.0) / np.sqrt((var + F32(eps)).astype(F32))).astype(F32)
     g = np.stack([np.asarray(qg), np.asarray(kg)]).astype(F32)[None, :, None, :]
     b = np.stack([np.asarray(qb), np.asarray(kb)]).astype(F32)[None, :, None, :]

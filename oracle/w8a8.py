@@ -26,7 +26,7 @@ with --use_fast_math, whose approximations are not reproduced); tanh of the
 GELU evaluated in float64 and rounded to fp32.  Row reductions use the
 kernel's fixed order (``row_sum_f32``): element chunks of 8 are dealt to 64
 lanes (lane l owns chunks l, l+64, ...), each lane sums its elements in
-order, then a butterfly over lane distances 32, 16, 8, 4, 2, 1.
+order, then a butterfly over lane distances 1, 2, 4, 8, 16, 32.
 
 Pinning (tests/test_oracle_w8a8.py): known answers (x = k*amax/127 -> k,
 amax = 0 -> 0, saturation, half-even ties), float64 LayerNorm/RMSNorm within
@@ -69,7 +69,7 @@ def row_sum_f32(v: np.ndarray) -> np.ndarray:
         for e in range(CHUNK):
             acc = (acc + p[:, j, :, e]).astype(F32)
     lane = np.arange(LANES)
-    for off in (32, 16, 8, 4, 2, 1):
+    for off in (1, 2, 4, 8, 16, 32):
         acc = (acc + acc[:, lane ^ off]).astype(F32)
     return acc[:, 0]
 

@@ -10,7 +10,7 @@
 // one rounding each, no contraction into FMA (pragma below); IEEE division and
 // square root; row reductions in a fixed order -- chunk c (8 elements) of a
 // row belongs to lane c % 64, each lane accumulates its elements in order,
-// then a butterfly over lane distances 32, 16, 8, 4, 2, 1.
+// then a butterfly over lane distances 1, 2, 4, 8, 16, 32.
 #include "common.h"
 
 #pragma clang fp contract(off)
@@ -62,35 +62,71 @@ __device__ __forceinline__ void store8(void* base, size_t e, const float (&v)[8]
 }
 
 // cvt.rni.sat.s8 semantics: round half to even, saturate, NaN -> 0.
+// v_cvt_i32_f32 already maps NaN to 0 and saturates out-of-range values, so
+// rint + convert + integer clamp (v_med3_i32) is the whole operation.  The
+// convert is inline asm: a C++ float -> int cast of NaN or of an
+// out-of-range value is undefined, and the hardware behaviour is the contract.
 __device__ __forceinline__ int sat_s8(float v) {
-  float r = __builtin_rintf(v);
-  r = r < -128.0f ? -128.0f : r;
-  r = r > 127.0f ? 127.0f : r;
-  return (v != v) ? 0 : (int)r;
+  int i;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(__builtin_rintf(v)));
+  return i < -128 ? -128 : (i > 127 ? 127 : i);
+}
+
+// four int8 (low bytes of a, b, c, d) -> one word, a in the low byte
+__device__ __forceinline__ uint32_t pack_s8x4(int a, int b, int c, int d) {
+  const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);  // [a0, b0, 0, 0]
+  const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);  // [c0, d0, 0, 0]
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);                                 // [a0, b0, c0, d0]
 }
 
 __device__ __forceinline__ void store_q8(int8_t* q, size_t e, const float (&t)[8], float mul) {
-  uint32_t lo = 0, hi = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) lo |= (uint32_t)(sat_s8(t[i] * mul) & 0xFF) << (8 * i);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) hi |= (uint32_t)(sat_s8(t[4 + i] * mul) & 0xFF) << (8 * i);
+  const uint32_t lo = pack_s8x4(sat_s8(t[0] * mul), sat_s8(t[1] * mul), sat_s8(t[2] * mul), sat_s8(t[3] * mul));
+  const uint32_t hi = pack_s8x4(sat_s8(t[4] * mul), sat_s8(t[5] * mul), sat_s8(t[6] * mul), sat_s8(t[7] * mul));
   *reinterpret_cast<uint2*>(q + e) = make_uint2(lo, hi);
 }
 
+// Cross-lane steps without LDS round trips: DPP within 16-lane rows, the
+// gfx950 permlane swaps across rows.  Each returns the partner lane's value
+// for the step's pairing; after steps 1..k every 2^k-lane group holds one
+// value, which is what lets the mirrors stand in for xor 4 and xor 8.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// x[l ^ 16] (v_permlane16_swap: rows 1 and 3 of the first operand trade
+// places with rows 0 and 2 of the second) and x[l ^ 32] (v_permlane32_swap).
+// Inline asm with the VALU -> permlane hazard covered by s_nop.
+__device__ __forceinline__ float xor16(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return (threadIdx.x & 16) ? a : b;
+}
+__device__ __forceinline__ float xor32(float v) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  return (threadIdx.x & 32) ? a : b;
+}
+
+// Butterfly over lane distances 1, 2, 4, 8, 16, 32 (every lane ends with the
+// wave total; the pairing is exact, so the fp32 result is the same on every
+// lane and equals the oracle's lane tree).
 __device__ __forceinline__ float bfly_sum(float v) {
-  v = v + __shfl_xor(v, 32);
-  v = v + __shfl_xor(v, 16);
-  v = v + __shfl_xor(v, 8);
-  v = v + __shfl_xor(v, 4);
-  v = v + __shfl_xor(v, 2);
-  v = v + __shfl_xor(v, 1);
+  v = v + dpp<0xB1>(v);   // quad_perm [1,0,3,2]: l ^ 1
+  v = v + dpp<0x4E>(v);   // quad_perm [2,3,0,1]: l ^ 2
+  v = v + dpp<0x141>(v);  // row_half_mirror: l ^ 4 once quads are uniform
+  v = v + dpp<0x140>(v);  // row_mirror: l ^ 8 once 8-lane groups are uniform
+  v = v + xor16(v);
+  v = v + xor32(v);
   return v;
 }
 
 __device__ __forceinline__ float bfly_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, xor16(v));
+  v = fmaxf(v, xor32(v));
   return v;
 }
 
@@ -163,7 +199,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict_
 // layernorm.cu:20-151 (rms_norm_general): mean and E[x^2] in fp32,
 // var = E[x^2] - mean^2, y = ((x - mean) * rs) * g (+ b).  Per token: amax over
 // y rounded to the input type (floor 1e-6 in that type), int8 from the fp32 y.
-// Per tensor: int8 = sat(rint(float(T(y)) * scale)), no beta.
+// Per tensor: int8 = sat(rint(float(T(y)) * scale)), no beta.  amax is taken
+// over |y| in fp32 and rounded once: rounding to the storage type is
+// monotonic and odd, so that equals the max over the rounded values.
 template <int DT, int J, bool PER_TOKEN>
 __global__ __launch_bounds__(256) void ln_quant_kernel(const void* __restrict__ x, const void* __restrict__ gamma,
                                                        const void* __restrict__ beta, int8_t* __restrict__ q,
@@ -177,7 +215,7 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(const void* __restrict__ 
   const float mean = s / (float)D;
   const float var = s2 / (float)D - mean * mean;
   const float rs = 1.0f / __builtin_sqrtf(var + eps);
-  float amax = round_to<DT>(1e-6f);
+  float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     if (!ok[j]) continue;
@@ -191,11 +229,11 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(const void* __restrict__ 
       t = t * g[e];
       if constexpr (PER_TOKEN) t = t + b[e];
       v[j][e] = t;
-      if constexpr (PER_TOKEN) amax = fmaxf(amax, __builtin_fabsf(round_to<DT>(t)));
+      if constexpr (PER_TOKEN) amax = fmaxf(amax, __builtin_fabsf(t));
     }
   }
   if constexpr (PER_TOKEN) {
-    amax = bfly_max(amax);
+    amax = fmaxf(round_to<DT>(1e-6f), round_to<DT>(bfly_max(amax)));
     const float dyn = 127.0f / amax;
 #pragma unroll
     for (int j = 0; j < J; ++j)

@@ -107,60 +107,81 @@ __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict_
 
 // VGGT attention prologue, fused: per-head LayerNorm of q and k (qk-norm,
 // affine, over the 64 head dims), rounded to fp16, then the 2-D RoPE above,
-// in place in the fused qkv buffer.  One thread per (token, part, head) row of
-// 64 values; statistics in fp32 with the row summed in index order, two-pass
-// variance; one rounding per fp32 operation.
+// in place in the fused qkv buffer.  Eight lanes per (token, part, head) row:
+// lane j of the row holds dims 8j..8j+7 (one 16-byte load and store), so a
+// wave moves 8 whole rows per instruction.  Statistics in fp32: each lane sums
+// its 8 values in order, then a butterfly over lanes j ^ 1, j ^ 2, j ^ 4
+// (DPP, no LDS); two-pass variance; one rounding per fp32 operation.  The
+// rotation partner of dim d (d +- 16 in its half) sits in lane j ^ 2.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float sum8_lanes(float v) {
+  v = v + dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]: j ^ 1
+  v = v + dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]: j ^ 2
+  v = v + dpp_f<0x141>(v);  // row_half_mirror: j ^ 4 once quads are uniform
+  return v;
+}
+
+constexpr int QKN_ROWS_PER_WG = 32;  // 4 waves x 8 rows
+
 __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
     uint16_t* __restrict__ qkv, const int* __restrict__ pos, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, int P, const uint16_t* __restrict__ qg, const uint16_t* __restrict__ qb,
     const uint16_t* __restrict__ kg, const uint16_t* __restrict__ kb, float eps, int T, int H, long tok_stride) {
-  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (long)T * 2 * H) return;
-  const int tok = (int)(gid / (2 * H));
-  const int r = (int)(gid % (2 * H));
+  const long grow = (long)blockIdx.x * QKN_ROWS_PER_WG + (threadIdx.x >> 3);
+  const bool live = grow < (long)T * 2 * H;
+  const long rowc = live ? grow : 0;          // dead lanes shadow row 0 and store nothing
+  const int j = threadIdx.x & 7;
+  const int tok = (int)(rowc / (2 * H));
+  const int r = (int)(rowc % (2 * H));
   const int part = r / H, head = r % H;
   uint16_t* row = qkv + (size_t)tok * tok_stride + (size_t)part * H * 64 + (size_t)head * 64;
-  float x[64];
+  float x[8];
+  {
+    const f16x8 v = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(row)[j]);
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const f16x8 v = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(row)[c]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[8 * c + e] = (float)v[e];
+    for (int e = 0; e < 8; ++e) x[e] = (float)v[e];
   }
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 64; ++i) s = s + x[i];
-  const float mean = s / 64.0f;
+  for (int e = 0; e < 8; ++e) s = s + x[e];
+  const float mean = sum8_lanes(s) / 64.0f;
   float s2 = 0.f;
 #pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    x[i] = x[i] - mean;
-    s2 = s2 + x[i] * x[i];
+  for (int e = 0; e < 8; ++e) {
+    x[e] = x[e] - mean;
+    s2 = s2 + x[e] * x[e];
   }
-  const float rs = 1.0f / __builtin_sqrtf(s2 / 64.0f + eps);
-  const uint16_t* g = part ? kg : qg;
-  const uint16_t* b = part ? kb : qb;
+  const float rs = 1.0f / __builtin_sqrtf(sum8_lanes(s2) / 64.0f + eps);
+  const f16x8 g = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(part ? kg : qg)[j]);
+  const f16x8 b = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(part ? kb : qb)[j]);
 #pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    const float t = (x[i] * rs) * to_f32(g[i], false) + to_f32(b[i], false);
-    x[i] = (float)__builtin_bit_cast(_Float16, from_f32<false>(t));   // q_norm output is fp16
+  for (int e = 0; e < 8; ++e) {
+    const float t = (x[e] * rs) * (float)g[e] + (float)b[e];
+    x[e] = (float)__builtin_bit_cast(_Float16, from_f32<false>(t));   // q_norm output is fp16
   }
-  f16x8 o[8];
+  // 2-D RoPE: lanes 0-3 hold the y half (dims 0..31), 4-7 the x half; within a
+  // half, lanes with (j & 2) == 0 hold dims i < 16 and rotate against j ^ 2.
+  const int half = j >> 2;
+  int p = pos[2 * tok + half];
+  p = p < 0 ? 0 : (p >= P ? P - 1 : p);
+  const int i0 = 8 * (j & 1);
+  const float4* cp = reinterpret_cast<const float4*>(cos_t + p * 16 + i0);
+  const float4* sp = reinterpret_cast<const float4*>(sin_t + p * 16 + i0);
+  const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+  const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  const bool lo = (j & 2) == 0;
+  f16x8 o;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    int p = pos[2 * tok + half];
-    p = p < 0 ? 0 : (p >= P ? P - 1 : p);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float c = cos_t[p * 16 + i], sn = sin_t[p * 16 + i];
-      const float a = x[32 * half + i], bb = x[32 * half + 16 + i];
-      const int d0 = 32 * half + i, d1 = d0 + 16;
-      o[d0 >> 3][d0 & 7] = __builtin_bit_cast(_Float16, from_f32<false>(a * c - bb * sn));
-      o[d1 >> 3][d1 & 7] = __builtin_bit_cast(_Float16, from_f32<false>(bb * c + a * sn));
-    }
+  for (int e = 0; e < 8; ++e) {
+    const float other = dpp_f<0x4E>(x[e]);   // partner lane j ^ 2
+    const float v = lo ? x[e] * cs[e] - other * sn[e] : x[e] * cs[e] + other * sn[e];
+    o[e] = __builtin_bit_cast(_Float16, from_f32<false>(v));
   }
-#pragma unroll
-  for (int c = 0; c < 8; ++c) reinterpret_cast<uint4*>(row)[c] = __builtin_bit_cast(uint4, o[c]);
+  if (live) reinterpret_cast<uint4*>(row)[j] = __builtin_bit_cast(uint4, o);
 }
 
 }  // namespace qv
@@ -177,8 +198,14 @@ extern "C" int qv_qknorm_rope2d(void* qkv, const int32_t* positions, const float
                "null pointer argument");
   QV_CHECK_ARG(token_stride % 8 == 0 && token_stride >= 2 * H * 64 && ((uintptr_t)qkv % 16) == 0,
                "qkv rows must be 16-byte aligned and hold q and k");
-  const long total = T * 2 * H;
-  hipLaunchKernelGGL(qknorm_rope2d_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+  QV_CHECK_ARG(((uintptr_t)cos_table % 16) == 0 && ((uintptr_t)sin_table % 16) == 0 &&
+                   ((uintptr_t)q_gamma % 16) == 0 && ((uintptr_t)q_beta % 16) == 0 &&
+                   ((uintptr_t)k_gamma % 16) == 0 && ((uintptr_t)k_beta % 16) == 0,
+               "tables and norm weights must be 16-byte aligned");
+  const long rows = T * 2 * H;
+  QV_CHECK_ARG(rows / QKN_ROWS_PER_WG < INT32_MAX, "too many rows");
+  hipLaunchKernelGGL(qknorm_rope2d_kernel, dim3((unsigned)((rows + QKN_ROWS_PER_WG - 1) / QKN_ROWS_PER_WG)),
+                     dim3(256), 0, (hipStream_t)stream,
                      (uint16_t*)qkv, positions, cos_table, sin_table, (int)table_rows, (const uint16_t*)q_gamma,
                      (const uint16_t*)q_beta, (const uint16_t*)k_gamma, (const uint16_t*)k_beta, eps, (int)T, (int)H,
                      (long)token_stride);

@@ -3,13 +3,15 @@
     python qvggt_amd/profiling.py copy                 # traffic calibration
     python qvggt_amd/profiling.py gemm M K N [--gelu] [--reps R]
     python qvggt_amd/profiling.py aggregator [--frames S] [--w8a8]
+    python qvggt_amd/profiling.py attention [--frames S] [--global] [--reps R]
 
 ``copy`` launches one elementwise kernel that reads 512 MiB and writes
 512 MiB, three times: the FETCH_SIZE / WRITE_SIZE it reports per dispatch
 calibrate those counters against known byte counts.  ``gemm`` runs the W4A16
 linear (optionally with the fused bias + GELU epilogue) on seeded synthetic
 data; ``aggregator`` runs the VGGT aggregator forward twice (the first call
-warms up).  Every mode prints one line when done.
+warms up); ``attention`` runs frame (S sequences of 1374 tokens) or global
+(one sequence of S x 1374 tokens) attention over 16 heads on seeded data.  Every mode prints one line when done.
 """
 from __future__ import annotations
 
@@ -66,6 +68,21 @@ def _aggregator(S, w8a8):
     print(f"aggregator: S={S} w8a8={w8a8}, 2 forwards", flush=True)
 
 
+def _attention(S, glob, reps):
+    import torch
+
+    from qvggt_amd import awq_inference_engine as E
+
+    dev = torch.device("cuda:0")
+    L = S * 1374 if glob else 1374
+    qkv = torch.randn(S * 1374, 3, 16, 64, generator=torch.Generator().manual_seed(0)).half().to(dev)
+    out = torch.empty(S * 1374, 16, 64, dtype=torch.float16, device=dev)
+    for _ in range(reps):
+        E.attention(qkv[:, 0], qkv[:, 1], qkv[:, 2], L, out=out)
+    torch.cuda.synchronize()
+    print(f"attention: S={S} global={glob}, {reps} launches", flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -79,11 +96,17 @@ def main(argv=None):
     a = sub.add_parser("aggregator")
     a.add_argument("--frames", type=int, default=32)
     a.add_argument("--w8a8", action="store_true")
+    t = sub.add_parser("attention")
+    t.add_argument("--frames", type=int, default=8)
+    t.add_argument("--global", dest="glob", action="store_true")
+    t.add_argument("--reps", type=int, default=5)
     args = ap.parse_args(argv)
     if args.mode == "copy":
         _copy()
     elif args.mode == "gemm":
         _gemm(args.M, args.K, args.N, args.gelu, args.reps)
+    elif args.mode == "attention":
+        _attention(args.frames, args.glob, args.reps)
     else:
         _aggregator(args.frames, args.w8a8)
 
