@@ -189,6 +189,16 @@ def kernel_suite(dev):
     us = _time_graph(lambda i: E.rms_norm_general(q8[i % nb], xs[i % nb], g, b, sc[i % nb], 1e-6, True), 12)
     r["layernorm_quant_S32"] = {"us": round(us, 1), "GB/s": round((3 * M * D + 2 * M) / us / 1e3, 1)}
     del ys, q8
+    # W8A8 MLP hidden: GELU + per-token quant at M = 10992, D = 4096 (reads x,
+    # writes int8 + the fp16 GELU copy + scales), 4 rotating sets of 450 MB
+    Mh, Dh = 8 * 1374, 4096
+    hx = [torch.randn(Mh, Dh, **f16) for _ in range(4)]
+    hq = [torch.empty(Mh, Dh, dtype=torch.int8, device=dev) for _ in range(4)]
+    ht = [torch.empty(Mh, Dh, **f16) for _ in range(4)]
+    hs = torch.empty(Mh, **f16)
+    us = _time_graph(lambda i: E.gelu_and_quant(hq[i % 4], hx[i % 4], hs, ht[i % 4]), 8)
+    r["gelu_quant_M10992x4096"] = {"us": round(us, 1), "GB/s": round((5 * Mh * Dh + 2 * Mh) / us / 1e3, 1)}
+    del hx, hq, ht
     qkv = [torch.randn(M, 3 * D, **f16) for _ in range(4)]    # 4 x 270 MB
     pos = torch.from_numpy(np.tile(np.array([[0, 0]] * 5 + [[i // 37 + 1, i % 37 + 1] for i in range(1369)],
                                              np.int32), (32, 1))).to(dev)

@@ -119,6 +119,24 @@ def test_gelu_and_quant_bit_exact(gpu, M, D):
     assert np.array_equal(q.cpu().numpy(), qr)
 
 
+def test_gelu_every_finite_fp16_input(gpu):
+    """The fp16 GELU (and its tanh table) on all 63488 finite fp16 values,
+    bit for bit against the oracle."""
+    from qvggt_amd import awq_inference_engine as E
+    bits = np.arange(0x10000, dtype=np.uint16)
+    x = bits.view(np.float16)
+    x = x[np.isfinite(x)].reshape(62, 1024)
+    q = torch.empty(x.shape, dtype=torch.int8, device=gpu)
+    s = torch.empty(x.shape[0], dtype=torch.float16, device=gpu)
+    tmp = torch.empty(x.shape, dtype=torch.float16, device=gpu)
+    E.gelu_and_quant(q, torch.from_numpy(x).to(gpu), s, tmp)
+    with np.errstate(over="ignore", invalid="ignore"):
+        qr, sr, tr = Q.gelu_and_quant(x)
+    assert np.array_equal(_bits(tmp), tr.view(np.int16))
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+    assert np.array_equal(q.cpu().numpy(), qr)
+
+
 # ------------------------------------------------------- normalisation
 @pytest.mark.parametrize("shape", [(4, 300, 1024), (2, 7, 4096), (1, 1, 64)])
 def test_layernorm_forward_cuda_rmsnorm_bit_exact(gpu, shape):
