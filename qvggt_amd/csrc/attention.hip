@@ -6,9 +6,11 @@
 // token-major with arbitrary token strides and head stride 64, so q, k and v
 // can be read straight out of the fused qkv projection output.
 //
-// Workgroup: 4 waves, 32 queries each (128 queries of one (sequence, head)).
-// Per 64-key tile a wave computes S^T = K Q^T (2 x 4 v_mfma_f32_32x32x16_f16),
-// the online softmax in registers, and O^T += V^T P^T (2 x 4 more MFMAs).
+// Workgroup: 4 waves, 64 queries each (256 queries of one (sequence, head)).
+// Per 64-key tile a wave computes S^T = K Q^T for its two 32-query blocks
+// (2 x 2 x 4 v_mfma_f32_32x32x16_f16, every K fragment read from LDS feeding
+// both blocks), the online softmax in registers, and O^T += V^T P^T (16 more
+// MFMAs, each V^T fragment again feeding both blocks).
 // The softmax is trimmed to what the MFMAs cannot hide: key masking only on
 // the last (partial) tile, one fma + exp2 per score, row sums by v_dot2 on
 // the fp16 P values, and a lazy rescale -- the reference maximum moves only
@@ -20,8 +22,9 @@
 //    max / sum.
 //  * P^T is the PV B operand without any shuffle: k-step s = 2kb + p takes
 //    registers 8p..8p+7 of block kb, i.e. keys 32kb + 16p + {0..3, 8..11} + 4h.
-//  * V^T (the A operand) is kept transposed in LDS ([dim][key], 136-byte
-//    rows) so each lane reads its 8 keys as two 8-byte loads.
+//  * V^T (the A operand) is kept transposed in LDS ([dim][key], 144-byte
+//    rows, keys of each 16-key group in k-slot order) so each lane reads its
+//    8 keys as one 16-byte load, conflict-free across 16-lane groups.
 //  * K tiles arrive by LDS DMA ([key][dim], 128-byte rows, 16-byte chunk c of
 //    row r at c ^ (r & 7) ^ ((r >> 3) & 1)); V tiles are register-staged one
 //    tile ahead and written transposed.
@@ -29,13 +32,22 @@
 
 namespace qv {
 
-constexpr int ATT_BQ = 128;   // queries per workgroup
-constexpr int ATT_BK = 64;    // keys per tile
-constexpr int VT_PITCH = 136; // bytes per V^T row (64 keys + 8 B pad)
+constexpr int ATT_QW = 64;                 // queries per wave (two 32-query blocks)
+constexpr int ATT_BQ = 4 * ATT_QW;         // queries per workgroup
+constexpr int ATT_BK = 64;                 // keys per tile
+constexpr int VT_PITCH = 144;              // bytes per V^T row: 64 keys + 16 B pad
 
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units: P <= 256 between rescales
 
 __device__ __forceinline__ int fk(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// V^T keeps each 16-key group in MFMA k-slot order: key k_in of a group sits
+// at 8*((k_in >> 2) & 1) + 4*((k_in >> 3) & 1) + (k_in & 3), so the 8 keys a
+// lane feeds one PV MFMA ({0..3, 8..11} + 4h) are 16 contiguous bytes.
+__device__ __forceinline__ int vt_slot(int key) {
+  const int k_in = key & 15;
+  return (key & ~15) + 8 * ((k_in >> 2) & 1) + 4 * ((k_in >> 3) & 1) + (k_in & 3);
+}
 
 // max / sum of x over lanes l and l ^ 32.  v_permlane32_swap exchanges the
 // upper half of its first operand with the lower half of its second; with
@@ -59,7 +71,7 @@ __device__ __forceinline__ float half_sum(float x) {
   return a + b;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attention_fwd_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ out, int L, int H, long q_ts, long kv_ts, long v_ts, long o_ts, float scale_log2) {
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][ATT_BK * 128];
@@ -70,20 +82,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
   const int qtiles = (L + ATT_BQ - 1) / ATT_BQ;
-  const int bid = blockIdx.x;
-  const int qt = bid % qtiles;
-  const int head = (bid / qtiles) % H;
-  const int seq = bid / (qtiles * H);
+  // consecutive q-tiles of one (sequence, head) share an XCD (and its L2),
+  // which then streams that head's K / V once for all of them
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = lid % qtiles;
+  const int head = (lid / qtiles) % H;
+  const int seq = lid / (qtiles * H);
   const long tok0 = (long)seq * L;
 
-  // ---- Q^T fragments (B operand of S^T = K Q^T): 4 k-steps of 16 dims
-  const int qi = qt * ATT_BQ + wave * 32 + l32;     // query index in the sequence
-  const int qc = qi < L ? qi : L - 1;
-  uint4 qf[4];
-  {
+  // ---- Q^T fragments (B operand of S^T = K Q^T): per query block, 4 k-steps of 16 dims
+  uint4 qf[2][4];
+  int qi[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    qi[qb] = qt * ATT_BQ + wave * ATT_QW + 32 * qb + l32;     // query index in the sequence
+    const int qc = qi[qb] < L ? qi[qb] : L - 1;
     const uint16_t* qp = q + (tok0 + qc) * q_ts + (long)head * 64;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const uint4*>(qp + 16 * s + 8 * h);
+    for (int s = 0; s < 4; ++s) qf[qb][s] = *reinterpret_cast<const uint4*>(qp + 16 * s + 8 * h);
   }
 
   // ---- K tile DMA: 8 x 1 KB per tile, 2 per wave; lane L lands at key
@@ -107,6 +123,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   };
   // ---- V tile staging: thread t owns keys 2*(t/8), +1 and dims 8*(t%8)..+7
   const int vkp = tid >> 3, vdg = tid & 7;
+  const int vcol = vt_slot(2 * vkp) * 2;     // byte column of the key pair (adjacent slots)
   const auto rsV = make_rsrc(v + tok0 * v_ts + (long)head * 64, (uint64_t)L * v_ts * 2);
   uint4 vreg[2];
   auto load_v = [&](int tile) {
@@ -121,20 +138,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     for (int e = 0; e < 8; ++e) {
       const uint32_t lo = (e & 1) ? (a[e >> 1] >> 16) : (a[e >> 1] & 0xFFFF);
       const uint32_t hi = (e & 1) ? (b[e >> 1] >> 16) : (b[e >> 1] & 0xFFFF);
-      *reinterpret_cast<uint32_t*>(&vt_lds[buf][(8 * vdg + e) * VT_PITCH + 4 * vkp]) = lo | (hi << 16);
+      *reinterpret_cast<uint32_t*>(&vt_lds[buf][(8 * vdg + e) * VT_PITCH + vcol]) = lo | (hi << 16);
     }
   };
 
   const int ntiles = (L + ATT_BK - 1) / ATT_BK;
-  f32x16 o[2];
+  f32x16 o[2][2];   // [query block][dim block]
 #pragma unroll
-  for (int db = 0; db < 2; ++db)
+  for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[qb][db][r] = 0.f;
   // m_use: the running reference maximum in log2 units.  It is only raised
   // when a tile's maximum exceeds it by more than RESCALE_SLACK, so P values
   // stay <= 2^RESCALE_SLACK and most tiles skip the O rescale.
-  float m_use = -INFINITY, l_run = 0.f;
+  float m_use[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
   const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
   auto tile = [&](int j, bool mask) {
@@ -144,9 +163,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       issue_k(j + 1, buf ^ 1);
       load_v(j + 1);
     }
-    // ---- S^T = K Q^T for the 64 keys of tile j (raw dot products)
+    // ---- S^T = K Q^T for the 64 keys of tile j, both query blocks (raw dot products)
     const uint8_t* kb_lds = k_lds[buf];
-    f32x16 sc[2];
+    f32x16 sc[2][2];   // [query block][key block]
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int row = 32 * kb + l32;
@@ -154,70 +173,73 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       for (int st = 0; st < 4; ++st) {
         const int c = 2 * st + h;
         const uint4 kf = *reinterpret_cast<const uint4*>(kb_lds + row * 128 + ((c ^ fk(row)) * 16));
-        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf),
-                                                       __builtin_bit_cast(f16x8, qf[st]),
-                                                       st == 0 ? f32x16{} : sc[kb], 0, 0, 0);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          sc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf),
+                                                             __builtin_bit_cast(f16x8, qf[qb][st]),
+                                                             st == 0 ? f32x16{} : sc[qb][kb], 0, 0, 0);
       }
     }
-    if (mask) {
-      const int key0 = j * ATT_BK + 4 * h;
+    uint4 pf[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      if (mask) {
+        const int key0 = j * ATT_BK + 4 * h;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (key0 + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[qb][kb][r] = -INFINITY;
+      }
+      // ---- tile maximum of this query (both lane halves hold 32 keys each)
+      float mx = sc[qb][0][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[qb][0][r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[qb][1][r]);
+      mx = half_max(mx) * scale_log2;
+      // ---- lazy rescale: wave-uniform branch, taken when any query's tile
+      // maximum exceeds its reference by more than the slack
+      const bool need = mx > m_use[qb] + RESCALE_SLACK;
+      if (__builtin_amdgcn_ballot_w64(need)) {
+        const float m_new = need ? mx : m_use[qb];
+        const float alpha = __builtin_amdgcn_exp2f(m_use[qb] - m_new);  // 0 on the first tile, 1 if !need
+        m_use[qb] = m_new;
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+      }
+      // ---- P = 2^(s * scale_log2 - m_use) in fp16, row sums from the fp16 values
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (key0 + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[kb][r] = -INFINITY;
-    }
-    // ---- tile maximum of this query (both lane halves hold 32 keys each)
-    float mx = sc[0][0];
+        for (int pp = 0; pp < 2; ++pp) {
+          uint32_t w[4];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[0][r]);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[1][r]);
-    mx = half_max(mx) * scale_log2;
-    // ---- lazy rescale: wave-uniform branch, taken when any query's tile
-    // maximum exceeds its reference by more than the slack
-    const bool need = mx > m_use + RESCALE_SLACK;
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      const float m_new = need ? mx : m_use;
-      const float alpha = __builtin_amdgcn_exp2f(m_use - m_new);  // 0 on the first tile, 1 if !need
-      m_use = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-    }
-    // ---- P = 2^(s * scale_log2 - m_use) in fp16, row sums from the fp16 values
-    uint4 pf[4];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * pp + 2 * e], scale_log2, -m_use));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * pp + 2 * e + 1], scale_log2, -m_use));
-          const f16x2 ph = {(_Float16)p0, (_Float16)p1};
-          l_run = __builtin_amdgcn_fdot2(ph, ones, l_run, false);
-          w[e] = __builtin_bit_cast(uint32_t, ph);
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][8 * pp + 2 * e], scale_log2, -m_use[qb]));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][8 * pp + 2 * e + 1], scale_log2, -m_use[qb]));
+            const f16x2 ph = {(_Float16)p0, (_Float16)p1};
+            l_run[qb] = __builtin_amdgcn_fdot2(ph, ones, l_run[qb], false);
+            w[e] = __builtin_bit_cast(uint32_t, ph);
+          }
+          pf[qb][2 * kb + pp] = make_uint4(w[0], w[1], w[2], w[3]);
         }
-        pf[2 * kb + pp] = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-    // ---- O^T += V^T P^T
+    }
+    // ---- O^T += V^T P^T: each V^T fragment (16 contiguous bytes) feeds both query blocks
     const uint8_t* vt = vt_lds[buf];
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
       const int d = 32 * db + l32;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const int kb = st >> 1, pp = st & 1;
-        const int kk = 32 * kb + 16 * pp + 4 * h;
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vt + d * VT_PITCH + kk * 2);
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vt + d * VT_PITCH + (kk + 8) * 2);
-        const uint4 vf = make_uint4(v0.x, v0.y, v1.x, v1.y);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
-                                                      __builtin_bit_cast(f16x8, pf[st]), o[db], 0, 0, 0);
+        const uint4 vf = *reinterpret_cast<const uint4*>(vt + d * VT_PITCH + (16 * st + 8 * h) * 2);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
+                                                            __builtin_bit_cast(f16x8, pf[qb][st]), o[qb][db], 0, 0, 0);
       }
     }
     if (more) {
@@ -237,19 +259,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   if (nfull < ntiles) tile(nfull, true);
 
   // ---- normalise and store: lane (h, q) holds dims 32db + 8*(r/4) + 4h + r%4
-  const float l_tot = half_sum(l_run);
-  const float inv = 1.0f / l_tot;
-  if (qi < L) {
-    uint16_t* op = out + (tok0 + qi) * o_ts + (long)head * 64;
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+  for (int qb = 0; qb < 2; ++qb) {
+    const float l_tot = half_sum(l_run[qb]);
+    const float inv = 1.0f / l_tot;
+    if (qi[qb] < L) {
+      uint16_t* op = out + (tok0 + qi[qb]) * o_ts + (long)head * 64;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        uint2 w;
-        w.x = pack2<false>(o[db][4 * g] * inv, o[db][4 * g + 1] * inv);
-        w.y = pack2<false>(o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-        *reinterpret_cast<uint2*>(op + 32 * db + 8 * g + 4 * h) = w;
-      }
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint2 w;
+          w.x = pack2<false>(o[qb][db][4 * g] * inv, o[qb][db][4 * g + 1] * inv);
+          w.y = pack2<false>(o[qb][db][4 * g + 2] * inv, o[qb][db][4 * g + 3] * inv);
+          *reinterpret_cast<uint2*>(op + 32 * db + 8 * g + 4 * h) = w;
+        }
+    }
   }
 }
 
