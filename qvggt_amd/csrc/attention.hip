@@ -22,12 +22,12 @@
 //    max / sum.
 //  * P^T is the PV B operand without any shuffle: k-step s = 2kb + p takes
 //    registers 8p..8p+7 of block kb, i.e. keys 32kb + 16p + {0..3, 8..11} + 4h.
-//  * V^T (the A operand) is kept transposed in LDS ([dim][key], 144-byte
-//    rows, keys of each 16-key group in k-slot order) so each lane reads its
-//    8 keys as one 16-byte load, conflict-free across 16-lane groups.
-//  * K tiles arrive by LDS DMA ([key][dim], 128-byte rows, 16-byte chunk c of
-//    row r at c ^ (r & 7) ^ ((r >> 3) & 1)); V tiles are register-staged one
-//    tile ahead and written transposed.
+//  * K and V tiles arrive by LDS DMA in their natural [key][dim] layout
+//    (128-byte rows; 16-byte chunk c of row r at c ^ fk(r) for K and
+//    c ^ fv(r) for V), one tile ahead.
+//  * V^T (the PV A operand) comes out of LDS through ds_read_b64_tr_b16: two
+//    transposed 8-byte reads give each lane its dim's 8 keys in k-slot order,
+//    with no register staging or transposed stores.
 #include "common.h"
 
 namespace qv {
@@ -35,18 +35,24 @@ namespace qv {
 constexpr int ATT_QW = 64;                 // queries per wave (two 32-query blocks)
 constexpr int ATT_BQ = 4 * ATT_QW;         // queries per workgroup
 constexpr int ATT_BK = 64;                 // keys per tile
-constexpr int VT_PITCH = 144;              // bytes per V^T row: 64 keys + 16 B pad
 
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units: P <= 256 between rescales
 
 __device__ __forceinline__ int fk(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-// V^T keeps each 16-key group in MFMA k-slot order: key k_in of a group sits
-// at 8*((k_in >> 2) & 1) + 4*((k_in >> 3) & 1) + (k_in & 3), so the 8 keys a
-// lane feeds one PV MFMA ({0..3, 8..11} + 4h) are 16 contiguous bytes.
-__device__ __forceinline__ int vt_slot(int key) {
-  const int k_in = key & 15;
-  return (key & ~15) + 8 * ((k_in >> 2) & 1) + 4 * ((k_in >> 3) & 1) + (k_in & 3);
+// V rows swizzle: 16-byte chunk c of key row r sits at c ^ fv(r).  The
+// transposed reads below touch 4 consecutive rows per 16-lane group; fv moves
+// rows r and r + 2 to opposite halves of the 128-byte row, so each 32-lane
+// half of a read covers all 64 banks once.
+__device__ __forceinline__ int fv(int r) { return 4 * ((r >> 1) & 1); }
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: within each 16-lane group, lane j = 4a + b receives
+// element b of the 8-byte segments addressed by lanes a, a + 4, a + 8, a + 12.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* p) {
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)(__attribute__((address_space(3))) uint8_t*)p);
+  return __builtin_bit_cast(uint2, r);
 }
 
 // max / sum of x over lanes l and l ^ 32.  v_permlane32_swap exchanges the
@@ -75,7 +81,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ out, int L, int H, long q_ts, long kv_ts, long v_ts, long o_ts, float scale_log2) {
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][ATT_BK * 128];
-  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[2][64 * VT_PITCH];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[2][ATT_BK * 128];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -121,27 +127,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 klds0 + buf * (ATT_BK * 128) + r0 * 128);
     }
   };
-  // ---- V tile staging: thread t owns keys 2*(t/8), +1 and dims 8*(t%8)..+7
-  const int vkp = tid >> 3, vdg = tid & 7;
-  const int vcol = vt_slot(2 * vkp) * 2;     // byte column of the key pair (adjacent slots)
+  // ---- V tile DMA, natural [key][dim] layout with the fv swizzle
   const auto rsV = make_rsrc(v + tok0 * v_ts + (long)head * 64, (uint64_t)L * v_ts * 2);
-  uint4 vreg[2];
-  auto load_v = [&](int tile) {
+  uint32_t v_voff[2];
 #pragma unroll
-    for (int e = 0; e < 2; ++e)
-      vreg[e] = buf_load16(rsV, (uint32_t)(((tile * ATT_BK + 2 * vkp + e) * v_ts + 8 * vdg) * 2), 0);
-  };
-  auto store_vt = [&](int buf) {
-    const uint32_t* a = reinterpret_cast<const uint32_t*>(&vreg[0]);
-    const uint32_t* b = reinterpret_cast<const uint32_t*>(&vreg[1]);
+  for (int w2 = 0; w2 < 2; ++w2) {
+    const int row = 8 * (2 * wave + w2) + (lane >> 3);
+    const int c = (lane & 7) ^ fv(row);
+    v_voff[w2] = (uint32_t)((lane >> 3) * v_ts * 2 + c * 16);
+  }
+  const uint32_t vlds0 = lds_addr(v_lds);
+  auto issue_v = [&](int tile, int buf) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t lo = (e & 1) ? (a[e >> 1] >> 16) : (a[e >> 1] & 0xFFFF);
-      const uint32_t hi = (e & 1) ? (b[e >> 1] >> 16) : (b[e >> 1] & 0xFFFF);
-      *reinterpret_cast<uint32_t*>(&vt_lds[buf][(8 * vdg + e) * VT_PITCH + vcol]) = lo | (hi << 16);
+    for (int w2 = 0; w2 < 2; ++w2) {
+      const int r0 = 8 * (2 * wave + w2);
+      lds_dma16(rsV, v_voff[w2], (uint32_t)((tile * ATT_BK + r0) * v_ts * 2),
+                vlds0 + buf * (ATT_BK * 128) + r0 * 128);
     }
   };
-
+  // Transposed V^T fragments: for k-step st (keys 16 st + {0..3, 8..11} + 4h
+  // in k-slot order) and dim block db, lane (group G = lane / 16, i = lane % 16)
+  // addresses key 16 st + 8 r + 4h + i / 4, dims 32 db + 16 (G & 1) + 4 (i & 3)
+  // for reads r = 0, 1; the transpose hands lane l32 its dim's 8 keys.
+  const int tr_key = 4 * h + ((lane & 15) >> 2);
+  const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   const int ntiles = (L + ATT_BK - 1) / ATT_BK;
   f32x16 o[2][2];   // [query block][dim block]
 #pragma unroll
@@ -161,7 +170,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const bool more = j + 1 < ntiles;
     if (more) {
       issue_k(j + 1, buf ^ 1);
-      load_v(j + 1);
+      issue_v(j + 1, buf ^ 1);
     }
     // ---- S^T = K Q^T for the 64 keys of tile j, both query blocks (raw dot products)
     const uint8_t* kb_lds = k_lds[buf];
@@ -229,30 +238,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
     // ---- O^T += V^T P^T: each V^T fragment (16 contiguous bytes) feeds both query blocks
-    const uint8_t* vt = vt_lds[buf];
+    const uint8_t* vb = v_lds[buf];
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
-      const int d = 32 * db + l32;
+      const int dim = 32 * db + tr_dim;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const uint4 vf = *reinterpret_cast<const uint4*>(vt + d * VT_PITCH + (16 * st + 8 * h) * 2);
+        uint2 vv[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int key = 16 * st + 8 * r + tr_key;
+          vv[r] = lds_read_tr16(vb + key * 128 + (((dim >> 3) ^ fv(key)) * 16) + ((dim >> 2) & 1) * 8);
+        }
+        const uint4 vf = make_uint4(vv[0].x, vv[0].y, vv[1].x, vv[1].y);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
           o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
                                                             __builtin_bit_cast(f16x8, pf[qb][st]), o[qb][db], 0, 0, 0);
       }
     }
-    if (more) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next K tile and V registers landed
-      store_vt(buf ^ 1);
-    }
+    if (more) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next K and V tiles landed
     lds_barrier();
   };
 
   issue_k(0, 0);
-  load_v(0);
+  issue_v(0, 0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  store_vt(0);
   lds_barrier();
   const int nfull = L / ATT_BK;        // tiles with every key valid
   for (int j = 0; j < nfull; ++j) tile(j, false);
