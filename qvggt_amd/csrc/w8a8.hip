@@ -81,24 +81,30 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0;
 
   const int fl = f8(l32);  // f(32*i + l32) == f(l32) for every i, and f(64*w + 32*j + l32) too
+  // Both k-steps' fragments are read up front (6 x b128 each), the second
+  // step's reads in flight while the first step's MFMAs issue; the fence keeps
+  // the compiler from sinking them next to their use.
   auto compute = [&](int st) {
     const uint8_t* base = lds + st * STAGE;
+    uint4 bw[2][NT], av[2][MT];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const uint32_t col = (uint32_t)(((2 * s + h) ^ fl) * 16);
-      uint4 bw[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j)
-        bw[j] = *reinterpret_cast<const uint4*>(base + A_BYTES + (64 * wave + 32 * j + l32) * 64 + col);
+        bw[s][j] = *reinterpret_cast<const uint4*>(base + A_BYTES + (64 * wave + 32 * j + l32) * 64 + col);
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const uint4 av = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 64 + col);
+      for (int i = 0; i < MT; ++i) av[s][i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 64 + col);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < NT; ++j)
-          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bw[j]),
-                                                            __builtin_bit_cast(i32x4, av), acc[j][i], 0, 0, 0);
-      }
-    }
+          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bw[s][j]),
+                                                            __builtin_bit_cast(i32x4, av[s][i]), acc[j][i], 0, 0, 0);
   };
 
   issue(0, 0);
