@@ -116,6 +116,22 @@ def quantize_w4(linear: nn.Linear, group: int = 128) -> WQLinear:
     return WQLinear.from_linear(linear, 4, group, scales=s.half(), zeros=z.half())
 
 
+def _linear(layer, x: torch.Tensor, epilogue: int, out: torch.Tensor) -> torch.Tensor:
+    """One linear of an AA block: ``WQLinear`` on the W4A16 kernels with the
+    bias (+ GELU) fused, or an unquantised fp16 ``nn.Linear`` (blocks a
+    checkpoint leaves in floating point, loader.py:320-362) through torch."""
+    if isinstance(layer, WQLinear):
+        return E.w4a16_linear(x, layer.qweight, layer.scales, layer.scaled_zeros, bias=layer.bias,
+                              epilogue=epilogue, out=out)
+    if layer.bias is not None:
+        y = torch.addmm(layer.bias, x, layer.weight.t(), out=out)
+    else:
+        y = torch.mm(x, layer.weight.t(), out=out)
+    if epilogue == QV_EPI_BIAS_GELU:
+        y.copy_(F.gelu(y))
+    return y
+
+
 # ------------------------------------------------------------------ blocks
 class LayerScale(nn.Module):
     def __init__(self, dim, init, dev=None):
@@ -138,7 +154,8 @@ class Mlp(nn.Module):
 
 
 class AABlock(nn.Module):
-    """Frame or global block with W4A16 (``WQLinear``) or W8A8 linears."""
+    """Frame or global block with W4A16 (``WQLinear``) or W8A8 linears; in the
+    W4 form any of the four linears may also be an fp16 ``nn.Linear``."""
 
     def __init__(self, qkv, proj, fc1, fc2, w8a8: bool, dev=None):
         super().__init__()
@@ -157,8 +174,7 @@ class AABlock(nn.Module):
         a = self.attn
         if not self.w8a8:
             h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, LN_EPS, out=ws["h"])
-            qkv = E.w4a16_linear(h, a.qkv.qweight, a.qkv.scales, a.qkv.scaled_zeros, bias=a.qkv.bias,
-                                 epilogue=QV_EPI_BIAS, out=ws["qkv"])
+            qkv = _linear(a.qkv, h, QV_EPI_BIAS, ws["qkv"])
         else:
             E.rms_norm_general(ws["q8"], x, self.norm1.weight, self.norm1.bias, ws["s8"], LN_EPS, True)
             qkv = a.qkv(ws["q8"], ws["s8"], out=ws["qkv"])
@@ -168,8 +184,7 @@ class AABlock(nn.Module):
         att = E.attention(v3[:, 0], v3[:, 1], v3[:, 2], seq_len, out=ws["att"].view(M, HEADS, HEAD_DIM))
         att = att.view(M, DIM)
         if not self.w8a8:
-            o = E.w4a16_linear(att, a.proj.qweight, a.proj.scales, a.proj.scaled_zeros, bias=a.proj.bias,
-                               epilogue=QV_EPI_BIAS, out=ws["o"])
+            o = _linear(a.proj, att, QV_EPI_BIAS, ws["o"])
         else:
             E.invoke_quant(ws["q8"], att, ws["s8"])
             o = a.proj(ws["q8"], ws["s8"], out=ws["o"])
@@ -177,10 +192,8 @@ class AABlock(nn.Module):
         m = self.mlp
         if not self.w8a8:
             h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, LN_EPS, out=ws["h"])
-            f = E.w4a16_linear(h, m.fc1.qweight, m.fc1.scales, m.fc1.scaled_zeros, bias=m.fc1.bias,
-                               epilogue=QV_EPI_BIAS_GELU, out=ws["f"])
-            o = E.w4a16_linear(f, m.fc2.qweight, m.fc2.scales, m.fc2.scaled_zeros, bias=m.fc2.bias,
-                               epilogue=QV_EPI_BIAS, out=ws["o"])
+            f = _linear(m.fc1, h, QV_EPI_BIAS_GELU, ws["f"])
+            o = _linear(m.fc2, f, QV_EPI_BIAS, ws["o"])
         else:
             E.rms_norm_general(ws["q8"], x, self.norm2.weight, self.norm2.bias, ws["s8"], LN_EPS, True)
             f = m.fc1(ws["q8"], ws["s8"], out=ws["f"])
@@ -275,6 +288,22 @@ class Aggregator(nn.Module):
         self._ws = {}
 
     # ---------------------------------------------------------- construction
+    @classmethod
+    @torch.no_grad()
+    def empty(cls, device="cuda", depth: int = DEPTH):
+        """fp16 aggregator with zero weights and plain ``nn.Linear`` AA linears,
+        the starting point of checkpoint loading (qvggt_amd.loader swaps the
+        quantised layers for ``WQLinear`` before the state dict goes in)."""
+        dev = torch.device(device)
+
+        def lin(k, n):
+            return nn.Linear(k, n, device=dev, dtype=torch.float16)
+
+        def block():
+            return AABlock(lin(DIM, 3 * DIM), lin(DIM, DIM), lin(DIM, MLP_DIM), lin(MLP_DIM, DIM), False, dev)
+
+        return cls([block() for _ in range(depth)], [block() for _ in range(depth)], False, dev, dino_depth=depth)
+
     @classmethod
     @torch.no_grad()
     def random(cls, w8a8: bool = False, seed: int = 0, device="cuda", depth: int = DEPTH):

@@ -114,3 +114,36 @@ def test_frame_vs_global_attention_scope(gpu):
         blk(b, L, pos, tables, ws)
         outs.append(torch.equal(a[:AG.TOKENS], b[:AG.TOKENS]))
     assert outs[0] and not outs[1]
+
+
+def test_checkpoint_roundtrip_forward_is_identical(gpu, tmp_path):
+    """An aggregator loaded from a QVGGT-style quantised checkpoint (some AA
+    linears W4, the rest fp16) runs bit for bit like the model it was saved
+    from; the fp16 linears take the torch path, the W4 ones the HIP kernels."""
+    from safetensors.torch import save_file
+    from qvggt_amd import aggregator as AG
+    from qvggt_amd import loader as LD
+    from qvggt_amd.awq.qmodule import WQLinear
+    src = AG.Aggregator.random(w8a8=False, seed=11, device=gpu, depth=2)
+    # frame block 0 stays fp16: replace its W4 linears by fp16 ones with the dequantised weights
+    b = src.frame_blocks[0]
+    from qvggt_amd import awq_inference_engine as E
+    for parent, name in ((b.attn, "qkv"), (b.attn, "proj"), (b.mlp, "fc1"), (b.mlp, "fc2")):
+        q = getattr(parent, name)
+        lin = torch.nn.Linear(q.in_features, q.out_features, device=gpu, dtype=torch.float16)
+        lin.weight.data.copy_(E.w4a16_dequantize(q.qweight, q.scales, q.scaled_zeros, q.in_features))
+        lin.bias.data.copy_(q.bias)
+        setattr(parent, name, lin)
+    sd = {"aggregator." + k: v.detach().cpu().contiguous() for k, v in src.state_dict().items()
+          if not k.startswith("img_")}
+    sd["camera_head.pose_branch.fc1.weight"] = torch.zeros(4, 4, dtype=torch.float16)
+    path = tmp_path / "ckpt.safetensors"
+    save_file(sd, str(path))
+    agg, rep = LD.load_quantized_aggregator(path, device=gpu, depth=2)
+    assert len(rep["replaced"]) == 12
+    assert isinstance(agg.frame_blocks[0].attn.qkv, torch.nn.Linear)
+    assert isinstance(agg.frame_blocks[1].attn.qkv, WQLinear)
+    img = torch.rand(2, 3, AG.IMG, AG.IMG, generator=torch.Generator().manual_seed(3)).half().to(gpu)
+    a, _ = src(img)
+    c, _ = agg(img)
+    assert torch.equal(a, c) and torch.isfinite(a.float()).all()
