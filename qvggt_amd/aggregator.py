@@ -20,7 +20,8 @@ reference's loader uses for the quantised layers
 Assumptions taken from the public VGGT design where the reference and the
 benchmark configs are silent: qk-norm on, LayerScale init 0.01 (AA blocks) and
 1e-5 (DINOv2), exact-erf GELU in the W4 path (the W8A8 path uses the
-reference's tanh gelu_and_quant), block LayerNorm eps 1e-6.
+reference's tanh gelu_and_quant), LayerNorm eps 1e-5 in the AA blocks
+(torch's default, which VGGT's blocks keep) and 1e-6 in DINOv2.
 
 Every hot op runs on libqvggt_hip.so; only the DINOv2 fp16 linears (plain
 GEMMs: hipBLASLt through torch), its GELU, the patch convolution and the
@@ -50,7 +51,8 @@ N_REG = 4
 SPECIALS = 1 + N_REG         # camera + registers
 TOKENS = SPECIALS + GRID * GRID   # 1374
 DEPTH = 24
-LN_EPS = 1e-6
+LN_EPS = 1e-6                 # DINOv2 patch-embed LayerNorms
+BLOCK_LN_EPS = 1e-5           # AA-block norm1 / norm2 / q_norm / k_norm
 HEAD_LAYERS = (4, 11, 17, 23)     # intermediate outputs VGGT's heads consume
 IMAGENET_MEAN = (0.485, 0.456, 0.406)
 IMAGENET_STD = (0.229, 0.224, 0.225)
@@ -143,8 +145,8 @@ class AAAttention(nn.Module):
     def __init__(self, qkv, proj, dev=None):
         super().__init__()
         self.qkv, self.proj = qkv, proj
-        self.q_norm = nn.LayerNorm(HEAD_DIM, eps=LN_EPS, device=dev, dtype=torch.float16)
-        self.k_norm = nn.LayerNorm(HEAD_DIM, eps=LN_EPS, device=dev, dtype=torch.float16)
+        self.q_norm = nn.LayerNorm(HEAD_DIM, eps=BLOCK_LN_EPS, device=dev, dtype=torch.float16)
+        self.k_norm = nn.LayerNorm(HEAD_DIM, eps=BLOCK_LN_EPS, device=dev, dtype=torch.float16)
 
 
 class Mlp(nn.Module):
@@ -160,10 +162,10 @@ class AABlock(nn.Module):
     def __init__(self, qkv, proj, fc1, fc2, w8a8: bool, dev=None):
         super().__init__()
         self.w8a8 = w8a8
-        self.norm1 = nn.LayerNorm(DIM, eps=LN_EPS, device=dev, dtype=torch.float16)
+        self.norm1 = nn.LayerNorm(DIM, eps=BLOCK_LN_EPS, device=dev, dtype=torch.float16)
         self.attn = AAAttention(qkv, proj, dev)
         self.ls1 = LayerScale(DIM, 0.01, dev)
-        self.norm2 = nn.LayerNorm(DIM, eps=LN_EPS, device=dev, dtype=torch.float16)
+        self.norm2 = nn.LayerNorm(DIM, eps=BLOCK_LN_EPS, device=dev, dtype=torch.float16)
         self.mlp = Mlp(fc1, fc2)
         self.ls2 = LayerScale(DIM, 0.01, dev)
 
@@ -173,13 +175,13 @@ class AABlock(nn.Module):
         M = x.shape[0]
         a = self.attn
         if not self.w8a8:
-            h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, LN_EPS, out=ws["h"])
+            h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, BLOCK_LN_EPS, out=ws["h"])
             qkv = _linear(a.qkv, h, QV_EPI_BIAS, ws["qkv"])
         else:
-            E.rms_norm_general(ws["q8"], x, self.norm1.weight, self.norm1.bias, ws["s8"], LN_EPS, True)
+            E.rms_norm_general(ws["q8"], x, self.norm1.weight, self.norm1.bias, ws["s8"], BLOCK_LN_EPS, True)
             qkv = a.qkv(ws["q8"], ws["s8"], out=ws["qkv"])
         E.qknorm_rope2d(qkv, pos, tables[0], tables[1], HEADS, a.q_norm.weight, a.q_norm.bias,
-                        a.k_norm.weight, a.k_norm.bias, LN_EPS)
+                        a.k_norm.weight, a.k_norm.bias, BLOCK_LN_EPS)
         v3 = qkv.view(M, 3, HEADS, HEAD_DIM)
         att = E.attention(v3[:, 0], v3[:, 1], v3[:, 2], seq_len, out=ws["att"].view(M, HEADS, HEAD_DIM))
         att = att.view(M, DIM)
@@ -191,11 +193,11 @@ class AABlock(nn.Module):
         x.addcmul_(o, self.ls1.gamma)
         m = self.mlp
         if not self.w8a8:
-            h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, LN_EPS, out=ws["h"])
+            h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, BLOCK_LN_EPS, out=ws["h"])
             f = _linear(m.fc1, h, QV_EPI_BIAS_GELU, ws["f"])
             o = _linear(m.fc2, f, QV_EPI_BIAS, ws["o"])
         else:
-            E.rms_norm_general(ws["q8"], x, self.norm2.weight, self.norm2.bias, ws["s8"], LN_EPS, True)
+            E.rms_norm_general(ws["q8"], x, self.norm2.weight, self.norm2.bias, ws["s8"], BLOCK_LN_EPS, True)
             f = m.fc1(ws["q8"], ws["s8"], out=ws["f"])
             E.gelu_and_quant(ws["q8f"], f, ws["s8"], ws["ftmp"])
             o = m.fc2(ws["q8f"], ws["s8"], out=ws["o"])

@@ -227,6 +227,74 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(
   }
 }
 
+// ------------------------------------------------- skinny-M MFMA kernel
+// For 16 < M <= 64 (and the upper GEMV range): one workgroup per 16 output
+// channels whose W waves split the 128-k groups round-robin, as in the GEMV,
+// but the products run on v_mfma_f32_16x16x32 with the dequantised weights
+// as the A operand (row = channel) and up to four 16-token column blocks of
+// activations as B, read with buffer loads straight from L2 (tokens >= M
+// fall outside the descriptor and read as zero).  Lane (g, l): channel
+// n0 + l, k-slots 32g + 8t .. +8 of step t, the slot map of the 128 x 128
+// kernel; accumulator block mb holds out[m = 16 mb + l][n = n0 + 4g + r].
+// Each weight byte is read once; the activations (M x K, at most 1 MiB at
+// K = 8192) stay L2-resident.  Wave partials are summed through LDS.
+template <bool BF16, int MB>
+__global__ __launch_bounds__(1024) void w4a16_skinny_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K, int epi) {
+  __shared__ f32x4 red[16][MB][64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const int n0 = blockIdx.x * 16;
+  const int n = n0 + li;
+  const int KT = K >> 7;
+  const uint32_t K2 = (uint32_t)K * 2;
+  const auto rsX = make_rsrc(x, (uint64_t)M * K2);
+  const uint32_t x_voff = (uint32_t)li * K2 + (uint32_t)g * 64;
+
+  f32x4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int kt = wave; kt < KT; kt += nwaves) {
+    const uint4 wq = *reinterpret_cast<const uint4*>(qw + qw_chunk_u32(n, kt, g, K));
+    const uint32_t s = scales[(size_t)kt * N + n];
+    const uint32_t z = zeros[(size_t)kt * N + n];
+    uint4 xb[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xb[mb][t] = buf_load16(rsX, x_voff, mb * 16 * K2 + kt * 256 + t * 16);
+    uint4 wf[4];
+    wf[0] = dq_frag<BF16, 0>(wq, s, z);
+    wf[1] = dq_frag<BF16, 1>(wq, s, z);
+    wf[2] = dq_frag<BF16, 2>(wq, s, z);
+    wf[3] = dq_frag<BF16, 3>(wq, s, z);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16<BF16>(wf[t], xb[mb][t], acc[mb]);
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) red[wave][mb][lane] = acc[mb];
+  __syncthreads();
+  for (int e = tid; e < MB * 256; e += blockDim.x) {
+    const int mb = e >> 8, l = (e >> 2) & 63, r = e & 3;
+    const int m = 16 * mb + (l & 15);
+    if (m >= M) continue;
+    float v = 0.f;
+    for (int w = 0; w < nwaves; ++w) v += red[w][mb][l][r];
+    const int nn = n0 + 4 * (l >> 4) + r;
+    if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU) v += to_f32(bias[nn], BF16);
+    if (epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU) v = gelu_erf(v);
+    out[(size_t)m * N + nn] = from_f32<BF16>(v);
+  }
+}
+
 // ---------------------------------------------------------- dequant kernel
 // One thread per (row n, 32-k chunk): writes 32 weights in natural k order.
 template <bool BF16>
@@ -281,7 +349,9 @@ static int launch_gemm_cfg(const void* x, const void* qw, const void* s, const v
 // and the 128 x 128 register-staged kernel; two workgroups run per CU (512
 // slots on 256 CUs).  Score = useful fraction of the occupied slot-rounds
 // times a per-tile efficiency prior (larger BM amortises the dequantisation
-// over more MFMAs).  QVGGT_W4_TILE=s128|s96|s64|n128 forces one (tuning).
+// over more MFMAs).  M <= 64 goes to the skinny kernel, whose grid covers the
+// channels instead of M x N tiles.  QVGGT_W4_TILE=s128|s96|s64|n128|skinny
+// forces one (tuning).
 static int w4_tile_override() {
   static int v = [] {
     const char* e = getenv("QVGGT_W4_TILE");
@@ -290,14 +360,30 @@ static int w4_tile_override() {
     if (!strcmp(e, "s96")) return 2;
     if (!strcmp(e, "s64")) return 3;
     if (!strcmp(e, "n128")) return 4;
+    if (!strcmp(e, "skinny")) return 5;
     return 0;
   }();
   return v;
 }
 
-static int w4_pick_tile(int M, int N) {
+// GEMV entry: the v_dot2 kernel up to M = 4, the skinny MFMA kernel from
+// M = 5 (QVGGT_W4_GEMV=dot|mfma forces one kernel for every M, tuning).
+static int w4_gemv_mfma_from() {
+  static int v = [] {
+    const char* e = getenv("QVGGT_W4_GEMV");
+    if (e && !strcmp(e, "dot")) return 17;
+    if (e && !strcmp(e, "mfma")) return 1;
+    return 5;
+  }();
+  return v;
+}
+
+static int w4_pick_tile(int M, int N, int K) {
+  // the skinny kernel addresses the activations with 32-bit buffer offsets
+  const bool skinny_ok = M <= 64 && (int64_t)M * K * 2 < ((int64_t)1 << 31);
   const int ov = w4_tile_override();
-  if (ov) return ov;
+  if (ov) return (ov == 5 && !skinny_ok) ? 1 : ov;
+  if (skinny_ok) return 5;
   const struct { int id, bm, bn; double prior; } cand[] = {
       {1, 128, 256, 1.00}, {2, 96, 256, 0.93}, {3, 64, 256, 0.82}, {4, 128, 128, 0.70}};
   const double slots = 512.0;
@@ -313,12 +399,17 @@ static int w4_pick_tile(int M, int N) {
 }
 
 template <bool BF16>
+static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
+                         void* out, int M, int N, int K, int epi, hipStream_t st);
+
+template <bool BF16>
 static int launch_gemm(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                        void* out, int M, int N, int K, int epi, hipStream_t st) {
-  switch (w4_pick_tile(M, N)) {
+  switch (w4_pick_tile(M, N, K)) {
     case 1: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 128, st);
     case 2: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 96, st);
     case 3: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 64, st);
+    case 5: return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st);
     default: return launch_gemm_cfg<BF16, 128, 128, 64, 64>(x, qw, s, z, bias, out, M, N, K, epi, st);
   }
 }
@@ -340,6 +431,24 @@ static int launch_gemv(const void* x, const void* qw, const void* s, const void*
   else QV_GEMV(16);
 #undef QV_GEMV
   return check_launch("w4a16_gemv");
+}
+
+template <bool BF16>
+static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
+                         void* out, int M, int N, int K, int epi, hipStream_t st) {
+  const int KT = K / 128;
+  const int waves = KT < 16 ? KT : 16;
+  const dim3 grid(N / 16), block(64 * waves);
+#define QV_SKINNY(MB)                                                                          \
+  hipLaunchKernelGGL((w4a16_skinny_kernel<BF16, MB>), grid, block, 0, st, (const uint16_t*)x,  \
+                     (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,              \
+                     (const uint16_t*)bias, (uint16_t*)out, M, N, K, epi)
+  if (M <= 16) QV_SKINNY(1);
+  else if (M <= 32) QV_SKINNY(2);
+  else if (M <= 48) QV_SKINNY(3);
+  else QV_SKINNY(4);
+#undef QV_SKINNY
+  return check_launch("w4a16_skinny");
 }
 
 static int check_common(const void* x, const void* qw, const void* s, const void* z, const void* bias,
@@ -386,6 +495,11 @@ extern "C" int qv_w4a16_gemv(const void* x, const void* qweight, const void* sca
   int rc = check_common(x, qweight, scales, scaled_zeros, bias, out, M, N, K, dtype, epilogue);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
+  if (M >= w4_gemv_mfma_from() && M * K * 2 < ((int64_t)1 << 31)) {
+    if (dtype == QV_BF16)
+      return launch_skinny<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+    return launch_skinny<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+  }
   if (dtype == QV_BF16)
     return launch_gemv<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
   return launch_gemv<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);

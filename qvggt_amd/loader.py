@@ -1,4 +1,4 @@
-"""Quantised-checkpoint loading for the VGGT aggregator.
+"""Quantised-checkpoint loading for the VGGT aggregator and camera head.
 
 The host-side half of "loads the same quantised checkpoints unchanged": the
 selection logic of the reference loader (qvggt/inference/loader.py), applied
@@ -12,6 +12,7 @@ as the checkpoint (``aggregator.frame_blocks.{i}.attn.qkv.qweight`` ...).
 * ``quantize_specified_blocks``      loader.py:364-400 (nn.Linear -> WQLinear(init_only))
 * ``merge_state_dicts``              loader.py:466-548
 * ``load_quantized_aggregator``      loader.py:550-600 for the aggregator part
+* ``load_quantized_camera_head``     the same for ``camera_head.*`` (W4 trunk)
 
 Files are read with loaders that execute nothing from the file: safetensors,
 or ``torch.load(..., weights_only=True)`` (the reference unpickles).
@@ -188,8 +189,36 @@ def read_state_dict(path) -> dict:
 
 
 def aggregator_state_dict(sd, prefix: str = PREFIX) -> OrderedDict:
-    """The ``aggregator.*`` entries of a VGGT state dict, prefix stripped."""
+    """The ``aggregator.*`` (or other ``prefix``) entries of a VGGT state dict, prefix stripped."""
     return OrderedDict((k[len(prefix):], v) for k, v in sd.items() if k.startswith(prefix))
+
+
+def _copy_into(model: nn.Module, sd, strict: bool, what: str):
+    """Copy a prefix-stripped state dict into ``model``; returns (missing, unused)."""
+    own = model.state_dict()
+    missing = [k for k in own if k not in sd and not k.startswith("img_")]
+    unused = [k for k in sd if k not in own]
+    if strict and missing:
+        raise KeyError(f"checkpoint lacks {len(missing)} {what} tensors, e.g. {missing[:4]}")
+    for k, v in sd.items():
+        if k in own:
+            if own[k].shape != v.shape:
+                raise ValueError(f"{k}: checkpoint shape {tuple(v.shape)} != model {tuple(own[k].shape)}")
+            own[k].copy_(v.to(own[k].dtype) if not k.endswith(".qweight") else v)
+    return missing, unused
+
+
+def _merged(quantized_path, model_path, quantize_type, frame_blocks, global_blocks, layer_types,
+            quantize_camera_head):
+    qsd = read_state_dict(quantized_path)
+    if checkpoint_is_self_contained(qsd):
+        lay = infer_quantization_layout(qsd)
+        frame_blocks, global_blocks, layer_types = lay["frame_blocks"], lay["global_blocks"], lay["layer_types"]
+        quantize_camera_head = lay["quantize_camera_head"]
+    osd = read_state_dict(model_path) if model_path is not None else None
+    merged, cict = merge_state_dicts(qsd, osd, quantize_type, frame_blocks, global_blocks, layer_types,
+                                     quantize_camera_head)
+    return merged, cict, frame_blocks, global_blocks, layer_types, quantize_camera_head
 
 
 @torch.no_grad()
@@ -205,24 +234,30 @@ def load_quantized_aggregator(quantized_path, model_path=None, device="cuda", de
     the aggregator does not use (``strict`` raises on missing ones)."""
     from .aggregator import Aggregator
 
-    qsd = read_state_dict(quantized_path)
-    if checkpoint_is_self_contained(qsd):
-        lay = infer_quantization_layout(qsd)
-        frame_blocks, global_blocks, layer_types = lay["frame_blocks"], lay["global_blocks"], lay["layer_types"]
-    osd = read_state_dict(model_path) if model_path is not None else None
-    merged, cict = merge_state_dicts(qsd, osd, quantize_type, frame_blocks, global_blocks, layer_types)
+    merged, cict, frame_blocks, global_blocks, layer_types, _ = _merged(
+        quantized_path, model_path, quantize_type, frame_blocks, global_blocks, layer_types, False)
     agg = Aggregator.empty(device=device, depth=depth)
     replaced = quantize_specified_blocks(agg, w_bit, group_size, quantize_type, frame_blocks, global_blocks,
                                          layer_types)
-    sd = aggregator_state_dict(merged)
-    own = agg.state_dict()
-    missing = [k for k in own if k not in sd and not k.startswith("img_")]
-    unused = [k for k in sd if k not in own]
-    if strict and missing:
-        raise KeyError(f"checkpoint lacks {len(missing)} aggregator tensors, e.g. {missing[:4]}")
-    for k, v in sd.items():
-        if k in own:
-            if own[k].shape != v.shape:
-                raise ValueError(f"{k}: checkpoint shape {tuple(v.shape)} != model {tuple(own[k].shape)}")
-            own[k].copy_(v.to(own[k].dtype) if not k.endswith(".qweight") else v)
+    missing, unused = _copy_into(agg, aggregator_state_dict(merged), strict, "aggregator")
     return agg, {"replaced": replaced, "unused": unused, "missing": missing, "cict_token": cict}
+
+
+@torch.no_grad()
+def load_quantized_camera_head(quantized_path, model_path=None, device="cuda", w_bit: int = 4,
+                               group_size: int = 128, quantize_camera_head: bool = True, strict: bool = True):
+    """Build the VGGT camera head for a QVGGT checkpoint: fp16 head, trunk
+    linears swapped for ``WQLinear`` when the checkpoint quantises them
+    (``camera_head.trunk.*.qweight``, loader.py:204-206, 338-344), merged
+    ``camera_head.*`` weights loaded.  Returns (head, report) like
+    ``load_quantized_aggregator``; ``report["cict_token"]`` carries the CICT
+    token if the checkpoint has one (the head does not use it)."""
+    from .camera_head import CameraHead
+
+    merged, cict, _, _, _, quantize_camera_head = _merged(
+        quantized_path, model_path, "specific_blocks", None, None, None, quantize_camera_head)
+    head = CameraHead.empty(device=device)
+    replaced = (quantize_specified_blocks(head, w_bit, group_size, quantize_camera_head=True,
+                                          prefix="camera_head.") if quantize_camera_head else [])
+    missing, unused = _copy_into(head, aggregator_state_dict(merged, "camera_head."), strict, "camera head")
+    return head, {"replaced": replaced, "unused": unused, "missing": missing, "cict_token": cict}

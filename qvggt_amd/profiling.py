@@ -4,6 +4,7 @@
     python qvggt_amd/profiling.py gemm M K N [--gelu] [--reps R]
     python qvggt_amd/profiling.py aggregator [--frames S] [--w8a8]
     python qvggt_amd/profiling.py attention [--frames S] [--global] [--reps R]
+    python qvggt_amd/profiling.py camera [--frames S] [--reps R]
 
 ``copy`` launches one elementwise kernel that reads 512 MiB and writes
 512 MiB, three times: the FETCH_SIZE / WRITE_SIZE it reports per dispatch
@@ -83,6 +84,26 @@ def _attention(S, glob, reps):
     print(f"attention: S={S} global={glob}, {reps} launches", flush=True)
 
 
+def _camera(S, reps):
+    import time
+
+    import torch
+
+    from qvggt_amd.camera_head import CameraHead
+
+    dev = torch.device("cuda:0")
+    head = CameraHead.random(seed=0, device=dev)
+    t = torch.randn(S, 2048, generator=torch.Generator().manual_seed(1)).half().to(dev)
+    head(t)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        head(t)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    print(f"camera: S={S}, {reps} forwards, {ms:.3f} ms per forward", flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -100,6 +121,9 @@ def main(argv=None):
     t.add_argument("--frames", type=int, default=8)
     t.add_argument("--global", dest="glob", action="store_true")
     t.add_argument("--reps", type=int, default=5)
+    c = sub.add_parser("camera")
+    c.add_argument("--frames", type=int, default=32)
+    c.add_argument("--reps", type=int, default=10)
     args = ap.parse_args(argv)
     if args.mode == "copy":
         _copy()
@@ -107,6 +131,8 @@ def main(argv=None):
         _gemm(args.M, args.K, args.N, args.gelu, args.reps)
     elif args.mode == "attention":
         _attention(args.frames, args.glob, args.reps)
+    elif args.mode == "camera":
+        _camera(args.frames, args.reps)
     else:
         _aggregator(args.frames, args.w8a8)
 

@@ -1,0 +1,47 @@
+"""VGGT camera head with a W4A16 trunk on the GPU against the float64 oracle
+(oracle/camera_head.py).
+
+S pose tokens make the trunk linears run at M = S: S = 1 and 4 take the
+W4A16 GEMV, S = 24 the MFMA GEMM.  Every iteration's activated pose encoding
+is compared; tolerance max|out - ref| / max|ref| <= 1e-2 (fp16 residual stream
+and activations vs the float64 reference with the same dequantised weights).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import camera_head as OC
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(mod):
+    return {k: v.detach().cpu().numpy() for k, v in mod.state_dict().items()}
+
+
+@pytest.mark.parametrize("S", [1, 4, 24])
+def test_camera_head_w4_matches_oracle(gpu, S):
+    from qvggt_amd.camera_head import CameraHead
+    head = CameraHead.random(seed=S, device=gpu)
+    t = np.random.default_rng(S).standard_normal((S, OC.DIM)).astype(np.float16)
+    outs = head(torch.from_numpy(t).to(gpu))
+    torch.cuda.synchronize()
+    p = _params(head)
+    ref = OC.camera_head(t.astype(np.float64), p)
+    assert len(outs) == len(ref) == 4
+    for i, (o, r) in enumerate(zip(outs, ref)):
+        got = o.cpu().numpy()
+        err = np.abs(got - r).max() / np.abs(r).max()
+        assert got.shape == (S, 9) and np.isfinite(got).all() and err <= 1e-2, (i, err)
+
+
+def test_camera_head_takes_camera_tokens_of_the_aggregator_output(gpu):
+    """The head reads the camera token (token 0) of each frame of the last
+    [frame | global] aggregator layer; frames stay independent of their order."""
+    from qvggt_amd.camera_head import CameraHead
+    head = CameraHead.random(seed=5, device=gpu)
+    layer = torch.randn(3, 20, OC.DIM, device=gpu).half()
+    a = head(CameraHead.pose_tokens(layer))[-1]
+    b = head(CameraHead.pose_tokens(layer[[2, 0, 1]]))[-1]
+    torch.cuda.synchronize()
+    assert (a[[2, 0, 1]] - b).abs().max().item() <= 1e-2 * a.abs().max().item()

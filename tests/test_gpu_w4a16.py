@@ -110,9 +110,11 @@ def test_gemm_3d_input_and_determinism(gpu):
     _check_gemm(y1, p, 512, 1024)
 
 
-def test_gemm_bf16(gpu):
+@pytest.mark.parametrize("M", [300, 40, 6])
+def test_gemm_bf16(gpu, M):
+    """bf16 on the MFMA GEMM (M = 300) and the skinny kernel (M = 40, 6)."""
     from qvggt_amd import awq_inference_engine as E
-    M, N, K = 300, 512, 1024
+    N, K = 512, 1024
     p = O.make_w4_problem(M, K, N, seed=21)
     xb, sc, sz = _bf16_problem(p)
     x = torch.from_numpy(xb.view(np.int16)).to(gpu).view(torch.bfloat16).view(M, K)
@@ -124,6 +126,19 @@ def test_gemm_bf16(gpu):
     ref = O.bf16_bits_to_f32(xb) @ W.T
     err = O.rel_err(y.float().cpu().numpy(), ref)
     assert err <= TOL, err
+
+
+@pytest.mark.parametrize("M,N,K", [(24, 2048, 8192), (48, 6144, 2048), (64, 1024, 1024), (61, 48, 256),
+                                   (32, 8192, 2048)])
+def test_skinny_range(gpu, M, N, K):
+    """M <= 64 runs the skinny MFMA kernel: channels across the grid, 128-k
+    groups across the waves (several per wave at K = 8192), tokens past M
+    read as zero, partial sums reduced through LDS."""
+    from qvggt_amd import awq_inference_engine as E
+    p = O.make_w4_problem(M, K, N, seed=7 * M + K)
+    t = _to_dev(p, gpu)
+    y = E.gemm_forward_cuda_new(t["x"], t["qweight"], t["scales"], t["scaled_zeros"])
+    _check_gemm(y, p, N, K)
 
 
 @pytest.mark.parametrize("m", list(range(1, 8)))
@@ -146,7 +161,7 @@ def test_linear_small_m_routes_and_matches(gpu, M, N, K):
     _check_gemm(y, p, N, K)
 
 
-@pytest.mark.parametrize("M", [5, 700])
+@pytest.mark.parametrize("M", [3, 5, 50, 700])
 def test_epilogues_bias_gelu(gpu, M):
     from qvggt_amd import awq_inference_engine as E
     from qvggt_amd._lib import QV_EPI_BIAS, QV_EPI_BIAS_GELU

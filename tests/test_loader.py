@@ -98,3 +98,29 @@ def test_roundtrip_quantized_aggregator_checkpoint(tmp_path):
     assert got.keys() == ref.keys()
     for k in ref:
         assert got[k].dtype == ref[k].dtype and torch.equal(got[k], ref[k]), k
+
+
+def test_roundtrip_quantized_camera_head_checkpoint(tmp_path):
+    """A seeded camera head with a W4 trunk saved under ``camera_head.*`` loads
+    back bit for bit: the 16 trunk linears become WQLinear (inferred from the
+    ``camera_head.trunk.*.qweight`` keys), the rest stays fp16, and the CICT
+    token is reported (the head has no use for it)."""
+    from safetensors.torch import save_file
+    from qvggt_amd.camera_head import CameraHead
+    src = CameraHead.random(seed=3, device="cpu")
+    sd = {"camera_head." + k: v.contiguous() for k, v in src.state_dict().items()}
+    sd["aggregator.patch_embed.patch_embed.proj.weight"] = torch.zeros(2, dtype=torch.float16)
+    sd["aggregator.camera_token"] = torch.zeros(2, dtype=torch.float16)
+    sd["camera_head.cict_token"] = torch.arange(6, dtype=torch.float32)
+    path = tmp_path / "qvggt_w4_head.safetensors"
+    save_file(sd, str(path))
+    head, rep = LD.load_quantized_camera_head(path, device="cpu")
+    assert len(rep["replaced"]) == 16 and not rep["missing"]
+    assert rep["unused"] == ["cict_token"]          # kept in the merge (loader.py:480 pops only top-level keys)
+    assert all(n.startswith("camera_head.trunk.") for n in rep["replaced"])
+    assert torch.equal(rep["cict_token"], torch.arange(6, dtype=torch.float32))
+    assert isinstance(head.trunk[2].mlp.fc1, WQLinear) and isinstance(head.pose_branch.fc1, nn.Linear)
+    got, ref = head.state_dict(), src.state_dict()
+    assert got.keys() == ref.keys()
+    for k in ref:
+        assert got[k].dtype == ref[k].dtype and torch.equal(got[k], ref[k]), k
