@@ -79,6 +79,22 @@ int qv_w4a16_dequant(const void* qweight, const void* scales,
                      const void* scaled_zeros, void* out_w, int64_t N,
                      int64_t K, int dtype, void* stream);
 
+/*
+ * Quantise + pack: the buffers WQLinear.from_linear stores
+ * (awq/qmodule.py:225-329, pack_intweight at qmodule.py:43-99), computed on
+ * the GPU.  weight (N, K), scales and zeros (N, K/group_size) in `dtype`
+ * (zeros integer-valued).  q = round((w + z*s) / s) with every operation
+ * rounded to `dtype`, packed into qweight int16 (N/4, K) (low 16 bits of the
+ * unmasked nibble OR, as the reference); scales_out / scaled_zeros_out
+ * (calculate_zeros_width(K, group_size) * 8, N) = s^T and -(s * int(z))^T,
+ * zero-padded.  group_size 32, 64, >= 128 dividing K, or -1 (one group).
+ * Requires N % 4 == 0, K % 64 == 0; weight and qweight 16-byte aligned.
+ */
+int qv_w4a16_pack(const void* weight, const void* scales, const void* zeros,
+                  void* qweight, void* scales_out, void* scaled_zeros_out,
+                  int64_t N, int64_t K, int group_size, int dtype,
+                  void* stream);
+
 /* ------------------------------------------------------------ W8A8 family */
 
 /*

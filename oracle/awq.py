@@ -29,6 +29,10 @@ How each function is pinned (tests/test_oracle_awq.py):
   rounded once, plus the special cases q == z -> 0 and s = 1, sz = 0 -> q.
 * ``gemm_ref``: brute-force triple loop on tiny shapes, q == z -> y == 0,
   one-hot activations read back single weight columns.
+* ``quantize_intweight``: weights on an exactly representable grid
+  W = s (q - z) give back q; half-way cases round to even; and the same
+  expression evaluated with torch's own fp16 / bf16 tensor ops (a second
+  engine for the per-op rounding) agrees element for element.
 """
 from __future__ import annotations
 
@@ -108,6 +112,26 @@ def unpack_intweight(qweight: np.ndarray, N: int, K: int) -> np.ndarray:
     nib = np.stack([(q >> (4 * h)) & 0xF for h in range(4)], axis=-1)  # (rg,kb,r,c,f,e,h)
     nib = nib.transpose(0, 2, 1, 3, 6, 4, 5)  # (rg, r, kb, c, h, f, e)
     return nib.reshape(N, K).astype(np.uint8)
+
+
+def quantize_intweight(W: np.ndarray, s: np.ndarray, z: np.ndarray, group_size: int = 128,
+                       dtype=np.float16) -> np.ndarray:
+    """Integer weights of ``from_linear`` (qmodule.py:255-315):
+    q = round((W + z*s) / s) evaluated as the reference's 16-bit tensor ops do,
+    each op in float32 and rounded to ``dtype`` (fp16, or "bf16" given as
+    float32 values), torch.round = round half to even.  W (N, K); s, z
+    (N, K / group).  Returns int32 (N, K)."""
+    if dtype == np.float16:
+        r = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+    else:
+        r = lambda a: bf16_bits_to_f32(f64_to_bf16_bits(np.asarray(a, np.float32).astype(np.float64)))
+    W, s, z = (r(a) for a in (W, s, z))
+    K = W.shape[1]
+    gidx = np.arange(K) // (K if group_size == -1 else group_size)
+    sz = r(z * s)
+    t = r(W + sz[:, gidx])
+    u = r(t / s[:, gidx])
+    return np.rint(u).astype(np.int32)
 
 
 # ---------------------------------------------------------- scale / zero tables

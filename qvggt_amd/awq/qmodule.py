@@ -108,6 +108,8 @@ class WQLinear(nn.Module):
 
         scales, zeros: (out_features, in_features/group).  q = round((W + z*s)/s)
         per column (vectorised; element-wise identical to the reference loop).
+        On a GPU with weight, scales and zeros all fp16 (or all bf16) the whole
+        recipe runs as one HIP pass (``w4a16_pack``); otherwise in torch ops.
         """
         awq_linear = cls(w_bit, group_size, linear.in_features, linear.out_features,
                          linear.bias is not None, linear.weight.device,
@@ -115,6 +117,14 @@ class WQLinear(nn.Module):
         if init_only:
             return awq_linear
         assert scales is not None and zeros is not None
+        W = linear.weight.data
+        if (W.is_cuda and W.dtype in (torch.float16, torch.bfloat16) and scales.dtype == W.dtype
+                and zeros.dtype == W.dtype and W.shape[1] % 64 == 0):
+            awq_linear.qweight, awq_linear.scales, awq_linear.scaled_zeros = engine.w4a16_pack(
+                W, scales, zeros, group_size)
+            if linear.bias is not None:
+                awq_linear.bias = linear.bias.clone().to(W.dtype)
+            return awq_linear
         scale_zeros = zeros * scales
         dtype = scales.dtype
         gs = group_size if group_size != -1 else linear.in_features

@@ -200,6 +200,39 @@ def w4a16_dequantize(kernel: torch.Tensor, scales: torch.Tensor, zeros: torch.Te
     return out
 
 
+def w4a16_pack(weight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
+               group_size: int = 128):
+    """Quantise and pack fp16 / bf16 weights into the WQLinear buffers on the GPU.
+
+    weight (N, K), scales and zeros (N, K / group) in the weight's dtype (zeros
+    integer-valued).  Returns (qweight int16 (N/4, K), scales (rows, N),
+    scaled_zeros (rows, N)), element for element what ``WQLinear.from_linear``
+    (qmodule.py:225-329) stores: q = round((W + z*s) / s) in the model dtype,
+    AWQ-v2 packing, zero-padded transposed tables, scaled_zeros = -(s * z).
+    """
+    what = "w4a16_pack"
+    dev = _on_gpu(weight, scales, zeros, what=what)
+    dt = _dtype_code(weight, what)
+    if weight.dim() != 2:
+        _fail(f"{what}: weight must be (N, K)")
+    N, K = weight.shape
+    gs = K if group_size == -1 else group_size
+    if gs <= 0 or K % gs:
+        _fail(f"{what}: group size {group_size} does not divide K={K}")
+    for name, t in (("scales", scales), ("zeros", zeros)):
+        if t.dtype != weight.dtype or tuple(t.shape) != (N, K // gs):
+            _fail(f"{what}: {name} must be ({N}, {K // gs}) {weight.dtype}")
+    mult = 1 if group_size == -1 else {64: 2, 32: 4}.get(gs, 1)
+    rows = (-(-(-(-(K // gs) // 8)) // mult)) * mult * 8   # calculate_zeros_width(K, gs) * 8 (qmodule.py:13-41)
+    qweight = torch.empty(N // 4, K, dtype=torch.int16, device=dev)
+    s_out = torch.empty(rows, N, dtype=weight.dtype, device=dev)
+    sz_out = torch.empty(rows, N, dtype=weight.dtype, device=dev)
+    with _device(dev):
+        _lib.call("qv_w4a16_pack", _ptr(_contig(weight)), _ptr(_contig(scales)), _ptr(_contig(zeros)),
+                  _ptr(qweight), _ptr(s_out), _ptr(sz_out), N, K, group_size, dt, _stream(dev))
+    return qweight, s_out, sz_out
+
+
 # ------------------------------------------------------ ops with no source
 def gemm_forward_cuda(*args, **kwargs):
     """Legacy AWQ-v1 GEMM (pybind.cpp:19).  Its source (quantization/gemm_cuda_gen.cu)

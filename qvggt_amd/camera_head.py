@@ -22,7 +22,8 @@ the trunk blocks, 1e-6 for ``adaln_norm``.
 
 Per frame there is one pose token, so the trunk linears run at M = S: the
 W4A16 GEMV for S <= 16, the MFMA GEMM above.  Attention over S tokens with
-head_dim 128 is a few kFLOP and runs in fp32 through torch.  The CICT token
+head_dim 128 is a few kFLOP and runs in fp32 through torch.
+``GraphedCameraHead`` records the whole forward as one HIP graph.  The CICT token
 QVGGT's loader can attach (loader.py:224-246) has no public definition and is
 not modelled.
 """
@@ -67,7 +68,7 @@ class TrunkBlock(nn.Module):
         h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, LN_EPS)
         qkv = _linear(self.attn.qkv, h, QV_EPI_BIAS, torch.empty(S, 3 * DIM, dtype=x.dtype, device=x.device))
         q, k, v = qkv.float().view(S, 3, HEADS, HEAD_DIM).permute(1, 2, 0, 3)   # (H, S, 128) each
-        a = torch.softmax((q @ k.transpose(1, 2)) * HEAD_DIM ** -0.5, dim=-1) @ v
+        a = torch.softmax(torch.bmm(q, k.transpose(1, 2).contiguous()) * HEAD_DIM ** -0.5, dim=-1) @ v
         att = a.permute(1, 0, 2).reshape(S, DIM).half()
         o = _linear(self.attn.proj, att, QV_EPI_BIAS, torch.empty(S, DIM, dtype=x.dtype, device=x.device))
         x.addcmul_(o, self.ls1.gamma)
@@ -166,3 +167,35 @@ class CameraHead(nn.Module):
             pred = delta if pred is None else pred + delta
             outs.append(self.activate(pred))
         return outs
+
+
+class GraphedCameraHead:
+    """``CameraHead.forward`` for a fixed frame count S, recorded once as a HIP
+    graph and replayed: the head is ~400 small launches per call (4 iterations
+    x 4 trunk blocks of LayerNorm, four W4 linears at M = S, attention and
+    residual updates), so replay removes the host launch cost that otherwise
+    dominates at small S.  ``__call__(tokens)`` copies ``tokens`` (S, 2048)
+    into the graph's input buffer, replays, and returns the graph's output
+    tensors (overwritten by the next call; clone to keep them)."""
+
+    def __init__(self, head: CameraHead, S: int, num_iterations: int = 4):
+        dev = head.token_norm.weight.device
+        self.head, self.S = head, S
+        self.tokens = torch.zeros(S, DIM, dtype=torch.float16, device=dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                head(self.tokens, num_iterations)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.outs = head(self.tokens, num_iterations)
+
+    @torch.no_grad()
+    def __call__(self, tokens: torch.Tensor):
+        if tokens.shape != self.tokens.shape:
+            raise ValueError(f"GraphedCameraHead: recorded for {tuple(self.tokens.shape)} tokens, got {tuple(tokens.shape)}")
+        self.tokens.copy_(tokens)
+        self.graph.replay()
+        return self.outs

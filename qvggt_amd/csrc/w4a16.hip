@@ -228,8 +228,8 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(
 }
 
 // ------------------------------------------------- skinny-M MFMA kernel
-// For 16 < M <= 64 (and the upper GEMV range): one workgroup per 16 output
-// channels whose W waves split the 128-k groups round-robin, as in the GEMV,
+// For M <= 64: one workgroup per 16 NB output channels whose W waves split
+// the 128-k groups round-robin, as in the GEMV,
 // but the products run on v_mfma_f32_16x16x32 with the dequantised weights
 // as the A operand (row = channel) and up to four 16-token column blocks of
 // activations as B, read with buffer loads straight from L2 (tokens >= M
@@ -237,8 +237,11 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(
 // n0 + l, k-slots 32g + 8t .. +8 of step t, the slot map of the 128 x 128
 // kernel; accumulator block mb holds out[m = 16 mb + l][n = n0 + 4g + r].
 // Each weight byte is read once; the activations (M x K, at most 1 MiB at
-// K = 8192) stay L2-resident.  Wave partials are summed through LDS.
-template <bool BF16, int MB>
+// K = 8192) stay L2-resident but are re-read by every workgroup, so NB > 1
+// (each activation fragment feeding NB channel blocks) cuts that L2 -> CU
+// traffic by NB at the cost of NB-fold fewer workgroups.  Wave partials are
+// summed through LDS.
+template <bool BF16, int MB, int NB>
 __global__ __launch_bounds__(1024) void w4a16_skinny_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -249,49 +252,64 @@ __global__ __launch_bounds__(1024) void w4a16_skinny_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nwaves = blockDim.x >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const int n0 = blockIdx.x * 16;
-  const int n = n0 + li;
+  const int n0 = blockIdx.x * 16 * NB;
   const int KT = K >> 7;
   const uint32_t K2 = (uint32_t)K * 2;
   const auto rsX = make_rsrc(x, (uint64_t)M * K2);
   const uint32_t x_voff = (uint32_t)li * K2 + (uint32_t)g * 64;
 
-  f32x4 acc[MB];
+  f32x4 acc[NB][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[j][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   for (int kt = wave; kt < KT; kt += nwaves) {
-    const uint4 wq = *reinterpret_cast<const uint4*>(qw + qw_chunk_u32(n, kt, g, K));
-    const uint32_t s = scales[(size_t)kt * N + n];
-    const uint32_t z = zeros[(size_t)kt * N + n];
+    uint4 wq[NB];
+    uint32_t sj[NB], zj[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int n = n0 + 16 * j + li;
+      wq[j] = *reinterpret_cast<const uint4*>(qw + qw_chunk_u32(n, kt, g, K));
+      sj[j] = scales[(size_t)kt * N + n];
+      zj[j] = zeros[(size_t)kt * N + n];
+    }
     uint4 xb[MB][4];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int t = 0; t < 4; ++t) xb[mb][t] = buf_load16(rsX, x_voff, mb * 16 * K2 + kt * 256 + t * 16);
-    uint4 wf[4];
-    wf[0] = dq_frag<BF16, 0>(wq, s, z);
-    wf[1] = dq_frag<BF16, 1>(wq, s, z);
-    wf[2] = dq_frag<BF16, 2>(wq, s, z);
-    wf[3] = dq_frag<BF16, 3>(wq, s, z);
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int j = 0; j < NB; ++j) {
+      uint4 wf[4];
+      wf[0] = dq_frag<BF16, 0>(wq[j], sj[j], zj[j]);
+      wf[1] = dq_frag<BF16, 1>(wq[j], sj[j], zj[j]);
+      wf[2] = dq_frag<BF16, 2>(wq[j], sj[j], zj[j]);
+      wf[3] = dq_frag<BF16, 3>(wq[j], sj[j], zj[j]);
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16<BF16>(wf[t], xb[mb][t], acc[mb]);
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[j][mb] = mfma16<BF16>(wf[t], xb[mb][t], acc[j][mb]);
+    }
   }
+  // Cross-wave sums, one 16-channel block at a time through the same LDS.
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) red[wave][mb][lane] = acc[mb];
-  __syncthreads();
-  for (int e = tid; e < MB * 256; e += blockDim.x) {
-    const int mb = e >> 8, l = (e >> 2) & 63, r = e & 3;
-    const int m = 16 * mb + (l & 15);
-    if (m >= M) continue;
-    float v = 0.f;
-    for (int w = 0; w < nwaves; ++w) v += red[w][mb][l][r];
-    const int nn = n0 + 4 * (l >> 4) + r;
-    if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU) v += to_f32(bias[nn], BF16);
-    if (epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU) v = gelu_erf(v);
-    out[(size_t)m * N + nn] = from_f32<BF16>(v);
+  for (int j = 0; j < NB; ++j) {
+    if (j) __syncthreads();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) red[wave][mb][lane] = acc[j][mb];
+    __syncthreads();
+    for (int e = tid; e < MB * 256; e += blockDim.x) {
+      const int mb = e >> 8, l = (e >> 2) & 63, r = e & 3;
+      const int m = 16 * mb + (l & 15);
+      if (m >= M) continue;
+      float v = 0.f;
+      for (int w = 0; w < nwaves; ++w) v += red[w][mb][l][r];
+      const int nn = n0 + 16 * j + 4 * (l >> 4) + r;
+      if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU) v += to_f32(bias[nn], BF16);
+      if (epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU) v = gelu_erf(v);
+      out[(size_t)m * N + nn] = from_f32<BF16>(v);
+    }
   }
 }
 
@@ -315,6 +333,81 @@ __global__ __launch_bounds__(256) void w4a16_dequant_kernel(
   dst[1] = dq_frag<BF16, 1>(wq, s, z);
   dst[2] = dq_frag<BF16, 2>(wq, s, z);
   dst[3] = dq_frag<BF16, 3>(wq, s, z);
+}
+
+// ------------------------------------------------------------ pack kernels
+// WQLinear.from_linear on the GPU (qmodule.py:255-327).  One thread per (row
+// n, 32-k chunk): q = rint(r(r(w + r(z * s)) / s)), r() rounding to the model
+// dtype after every operation as the reference's 16-bit tensor ops do (each
+// computed in fp32, IEEE division, rint = round half to even as torch.round),
+// then the chunk's 32 values go into its 8 int16 of the AWQ-v2 layout: int16
+// 8c + 2f + e of row r in 64-k block kb holds k = 64kb + 32c + 8h + 2f + e at
+// bit 4h (the unmasked OR of qmodule.py:84-92, low 16 bits, so values outside
+// 0..15 pack exactly as the reference packs them).
+template <bool BF16>
+__device__ __forceinline__ float rnd16(float v) {
+  return to_f32(from_f32<BF16>(v), BF16);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void w4a16_pack_kernel(
+    const uint16_t* __restrict__ w, const uint16_t* __restrict__ s, const uint16_t* __restrict__ z,
+    uint16_t* __restrict__ qw, int N, int K, int gs, int G) {
+  const int chunks = K >> 5;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)N * chunks) return;
+  const int n = (int)(idx / chunks), ch = (int)(idx % chunks);
+  const int k0 = ch * 32, g = k0 / gs;
+  const float sf = to_f32(s[(size_t)n * G + g], BF16);
+  const float szf = rnd16<BF16>(to_f32(z[(size_t)n * G + g], BF16) * sf);
+  const uint4* src = reinterpret_cast<const uint4*>(w + (size_t)n * K + k0);
+  int q[32];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const uint4 u = src[v];
+    const uint32_t words[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float wf = to_f32((uint16_t)(words[i >> 1] >> (16 * (i & 1))), BF16);
+      const float t = rnd16<BF16>(wf + szf);
+      const float d = rnd16<BF16>(t / sf);
+      q[8 * v + i] = (int)__builtin_rintf(d);
+    }
+  }
+  uint32_t out[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {  // int16 pair (2p, 2p + 1) = f = p, e = 0 / 1
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      lo |= (uint32_t)q[8 * h + 2 * p] << (4 * h);
+      hi |= (uint32_t)q[8 * h + 2 * p + 1] << (4 * h);
+    }
+    out[p] = (lo & 0xFFFFu) | (hi << 16);
+  }
+  const int rg = n >> 2, r = n & 3, kb = k0 >> 6, c = (k0 >> 5) & 1;
+  *reinterpret_cast<uint4*>(qw + (size_t)rg * K + 64 * kb + 16 * r + 8 * c) =
+      make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// scales (rows, N) = s^T zero-padded; scaled_zeros = -r(float(s) * float(int(z)))
+// (qmodule.py:262-283, 317-327: zeros truncated to int32, product in fp32,
+// one rounding, negated), zero-padded.
+template <bool BF16>
+__global__ __launch_bounds__(256) void w4a16_pack_tables_kernel(
+    const uint16_t* __restrict__ s, const uint16_t* __restrict__ z, uint16_t* __restrict__ s_out,
+    uint16_t* __restrict__ sz_out, int N, int G, int rows) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)rows * N) return;
+  const int g = (int)(idx / N), n = (int)(idx % N);
+  uint16_t sv = 0, zv = 0;
+  if (g < G) {
+    sv = s[(size_t)n * G + g];
+    const float zi = (float)(int)to_f32(z[(size_t)n * G + g], BF16);
+    zv = from_f32<BF16>(to_f32(sv, BF16) * zi) ^ 0x8000u;
+  }
+  s_out[idx] = sv;
+  sz_out[idx] = zv;
 }
 
 // ------------------------------------------------------------- launchers
@@ -366,14 +459,14 @@ static int w4_tile_override() {
   return v;
 }
 
-// GEMV entry: the v_dot2 kernel up to M = 4, the skinny MFMA kernel from
-// M = 5 (QVGGT_W4_GEMV=dot|mfma forces one kernel for every M, tuning).
+// GEMV entry: the skinny MFMA kernel for every M (measured faster than the
+// v_dot2 GEMV from M = 1 on the VGGT shapes, where both are bound by load
+// latency, and up to 3.5x faster at M = 16, where the v_dot2 kernel is
+// VALU-bound).  QVGGT_W4_GEMV=dot keeps the v_dot2 kernel (comparison runs).
 static int w4_gemv_mfma_from() {
   static int v = [] {
     const char* e = getenv("QVGGT_W4_GEMV");
-    if (e && !strcmp(e, "dot")) return 17;
-    if (e && !strcmp(e, "mfma")) return 1;
-    return 5;
+    return (e && !strcmp(e, "dot")) ? 17 : 1;
   }();
   return v;
 }
@@ -433,20 +526,38 @@ static int launch_gemv(const void* x, const void* qw, const void* s, const void*
   return check_launch("w4a16_gemv");
 }
 
+// Channel blocks per skinny workgroup: NB = 2 from M = 5 when N >= 4096
+// (>= 128 workgroups remain), else 1 -- measured on the VGGT camera-head and
+// aggregator shapes, where NB = 4 never won (QVGGT_W4_SKINNY_NB=1|2 forces).
+static int w4_skinny_nb(int M, int N) {
+  static int ov = [] {
+    const char* e = getenv("QVGGT_W4_SKINNY_NB");
+    return e ? atoi(e) : 0;
+  }();
+  int nb = (ov == 1 || ov == 2) ? ov : (M > 4 && N >= 4096) ? 2 : 1;
+  if (N % (16 * nb)) nb = 1;
+  return nb;
+}
+
 template <bool BF16>
 static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                          void* out, int M, int N, int K, int epi, hipStream_t st) {
   const int KT = K / 128;
   const int waves = KT < 16 ? KT : 16;
-  const dim3 grid(N / 16), block(64 * waves);
-#define QV_SKINNY(MB)                                                                          \
-  hipLaunchKernelGGL((w4a16_skinny_kernel<BF16, MB>), grid, block, 0, st, (const uint16_t*)x,  \
-                     (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,              \
+  const int nb = w4_skinny_nb(M, N);
+  const dim3 grid(N / (16 * nb)), block(64 * waves);
+#define QV_SKINNY(MB, NB)                                                                         \
+  hipLaunchKernelGGL((w4a16_skinny_kernel<BF16, MB, NB>), grid, block, 0, st, (const uint16_t*)x, \
+                     (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,                 \
                      (const uint16_t*)bias, (uint16_t*)out, M, N, K, epi)
-  if (M <= 16) QV_SKINNY(1);
-  else if (M <= 32) QV_SKINNY(2);
-  else if (M <= 48) QV_SKINNY(3);
-  else QV_SKINNY(4);
+#define QV_SKINNY_M(NB)            \
+  if (M <= 16) QV_SKINNY(1, NB);   \
+  else if (M <= 32) QV_SKINNY(2, NB); \
+  else if (M <= 48) QV_SKINNY(3, NB); \
+  else QV_SKINNY(4, NB);
+  if (nb == 2) { QV_SKINNY_M(2) }
+  else { QV_SKINNY_M(1) }
+#undef QV_SKINNY_M
 #undef QV_SKINNY
   return check_launch("w4a16_skinny");
 }
@@ -522,4 +633,46 @@ extern "C" int qv_w4a16_dequant(const void* qweight, const void* scales, const v
     hipLaunchKernelGGL((w4a16_dequant_kernel<false>), grid, block, 0, st, (const uint32_t*)qweight,
                        (const uint16_t*)scales, (const uint16_t*)scaled_zeros, (uint16_t*)out_w, (int)N, (int)K);
   return check_launch("w4a16_dequant");
+}
+
+// Rows of the scale tables: calculate_zeros_width(K, group_size) * 8
+// (qmodule.py:13-41; group_size -1 = one group of K, multiplier 1).
+static int64_t w4_scale_rows(int64_t K, int group_size) {
+  const int gs = group_size == -1 ? (int)K : group_size;
+  int mult = 1;
+  if (group_size == 64) mult = 2;
+  else if (group_size == 32) mult = 4;
+  const int64_t base = (K / gs + 7) / 8;
+  return (base + mult - 1) / mult * mult * 8;
+}
+
+extern "C" int qv_w4a16_pack(const void* weight, const void* scales, const void* zeros, void* qweight,
+                             void* scales_out, void* scaled_zeros_out, int64_t N, int64_t K,
+                             int group_size, int dtype, void* stream) {
+  QV_CHECK_ARG(dtype == QV_F16 || dtype == QV_BF16, "unsupported dtype %d", dtype);
+  QV_CHECK_ARG(N > 0 && K > 0 && N % 4 == 0 && K % 64 == 0, "bad shape N=%lld K=%lld (need N %% 4 == 0, K %% 64 == 0)",
+               (long long)N, (long long)K);
+  QV_CHECK_ARG(N <= INT32_MAX && K <= INT32_MAX, "shape too large");
+  const int gs = group_size == -1 ? (int)K : group_size;
+  QV_CHECK_ARG(gs >= 32 && gs % 32 == 0 && K % gs == 0 && (gs >= 128 || gs == 64 || gs == 32),
+               "unsupported group size %d for K=%lld", group_size, (long long)K);
+  QV_CHECK_ARG(weight && scales && zeros && qweight && scales_out && scaled_zeros_out, "null pointer argument");
+  QV_CHECK_ARG(((uintptr_t)weight % 16) == 0 && ((uintptr_t)qweight % 16) == 0, "weight and qweight must be 16-byte aligned");
+  const int G = (int)(K / gs);
+  const int64_t rows = w4_scale_rows(K, group_size);
+  hipStream_t st = (hipStream_t)stream;
+  const size_t total = (size_t)N * (size_t)(K / 32), ttot = (size_t)rows * (size_t)N;
+  const dim3 block(256), grid((unsigned)((total + 255) / 256)), tgrid((unsigned)((ttot + 255) / 256));
+  if (dtype == QV_BF16) {
+    hipLaunchKernelGGL((w4a16_pack_kernel<true>), grid, block, 0, st, (const uint16_t*)weight,
+                       (const uint16_t*)scales, (const uint16_t*)zeros, (uint16_t*)qweight, (int)N, (int)K, gs, G);
+    hipLaunchKernelGGL((w4a16_pack_tables_kernel<true>), tgrid, block, 0, st, (const uint16_t*)scales,
+                       (const uint16_t*)zeros, (uint16_t*)scales_out, (uint16_t*)scaled_zeros_out, (int)N, G, (int)rows);
+  } else {
+    hipLaunchKernelGGL((w4a16_pack_kernel<false>), grid, block, 0, st, (const uint16_t*)weight,
+                       (const uint16_t*)scales, (const uint16_t*)zeros, (uint16_t*)qweight, (int)N, (int)K, gs, G);
+    hipLaunchKernelGGL((w4a16_pack_tables_kernel<false>), tgrid, block, 0, st, (const uint16_t*)scales,
+                       (const uint16_t*)zeros, (uint16_t*)scales_out, (uint16_t*)scaled_zeros_out, (int)N, G, (int)rows);
+  }
+  return check_launch("w4a16_pack");
 }

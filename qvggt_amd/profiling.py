@@ -4,7 +4,7 @@
     python qvggt_amd/profiling.py gemm M K N [--gelu] [--reps R]
     python qvggt_amd/profiling.py aggregator [--frames S] [--w8a8]
     python qvggt_amd/profiling.py attention [--frames S] [--global] [--reps R]
-    python qvggt_amd/profiling.py camera [--frames S] [--reps R]
+    python qvggt_amd/profiling.py camera [--frames S] [--reps R] [--graph]
 
 ``copy`` launches one elementwise kernel that reads 512 MiB and writes
 512 MiB, three times: the FETCH_SIZE / WRITE_SIZE it reports per dispatch
@@ -84,15 +84,17 @@ def _attention(S, glob, reps):
     print(f"attention: S={S} global={glob}, {reps} launches", flush=True)
 
 
-def _camera(S, reps):
+def _camera(S, reps, graph):
     import time
 
     import torch
 
-    from qvggt_amd.camera_head import CameraHead
+    from qvggt_amd.camera_head import CameraHead, GraphedCameraHead
 
     dev = torch.device("cuda:0")
     head = CameraHead.random(seed=0, device=dev)
+    if graph:
+        head = GraphedCameraHead(head, S)
     t = torch.randn(S, 2048, generator=torch.Generator().manual_seed(1)).half().to(dev)
     head(t)
     torch.cuda.synchronize()
@@ -101,7 +103,7 @@ def _camera(S, reps):
         head(t)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / reps
-    print(f"camera: S={S}, {reps} forwards, {ms:.3f} ms per forward", flush=True)
+    print(f"camera: S={S} graph={graph}, {reps} forwards, {ms:.3f} ms per forward", flush=True)
 
 
 def main(argv=None):
@@ -124,6 +126,7 @@ def main(argv=None):
     c = sub.add_parser("camera")
     c.add_argument("--frames", type=int, default=32)
     c.add_argument("--reps", type=int, default=10)
+    c.add_argument("--graph", action="store_true")
     args = ap.parse_args(argv)
     if args.mode == "copy":
         _copy()
@@ -132,7 +135,7 @@ def main(argv=None):
     elif args.mode == "attention":
         _attention(args.frames, args.glob, args.reps)
     elif args.mode == "camera":
-        _camera(args.frames, args.reps)
+        _camera(args.frames, args.reps, args.graph)
     else:
         _aggregator(args.frames, args.w8a8)
 

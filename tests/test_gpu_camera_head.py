@@ -45,3 +45,30 @@ def test_camera_head_takes_camera_tokens_of_the_aggregator_output(gpu):
     b = head(CameraHead.pose_tokens(layer[[2, 0, 1]]))[-1]
     torch.cuda.synchronize()
     assert (a[[2, 0, 1]] - b).abs().max().item() <= 1e-2 * a.abs().max().item()
+
+
+def test_graphed_camera_head_replays_match_eager(gpu):
+    """HIP-graph replay of the head: three replays on different inputs, with
+    eager work and synchronisation between them, each equal to the eager
+    forward on the same input; a repeated input replays bit for bit."""
+    from qvggt_amd.camera_head import CameraHead, GraphedCameraHead
+    head = CameraHead.random(seed=9, device=gpu)
+    S = 8
+    g = GraphedCameraHead(head, S)
+    gen = torch.Generator(device=gpu).manual_seed(0)
+    inputs = [torch.randn(S, OC.DIM, generator=gen, device=gpu).half() for _ in range(3)]
+    first = None
+    for i, t in enumerate(inputs):
+        want = [o.clone() for o in head(t)]
+        torch.cuda.synchronize()
+        got = [o.clone() for o in g(t)]
+        torch.cuda.synchronize()
+        for a, b in zip(got, want):
+            assert (a - b).abs().max().item() <= 1e-3 * b.abs().max().item(), i
+        if i == 0:
+            first = got
+    again = g(inputs[0])
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(again, first))
+    with pytest.raises(ValueError):
+        g(inputs[0][:4])

@@ -129,7 +129,7 @@ def test_gemm_bf16(gpu, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(24, 2048, 8192), (48, 6144, 2048), (64, 1024, 1024), (61, 48, 256),
-                                   (32, 8192, 2048)])
+                                   (32, 8192, 2048), (12, 4112, 256), (7, 8192, 1024)])
 def test_skinny_range(gpu, M, N, K):
     """M <= 64 runs the skinny MFMA kernel: channels across the grid, 128-k
     groups across the waves (several per wave at K = 8192), tokens past M

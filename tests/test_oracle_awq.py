@@ -289,3 +289,37 @@ def test_gelu_polynomial_matches_erf_gelu():
     assert _gelu_poly_f32(np.float32(0.0)) == 0.0
     assert _gelu_poly_f32(np.float32(25.0)) == np.float32(25.0)
     assert abs(_gelu_poly_f32(np.float32(-25.0))) < 1e-7
+
+
+def test_quantize_intweight_recovers_exact_grid():
+    rng = np.random.default_rng(5)
+    N, K = 32, 256
+    q = rng.integers(0, 16, (N, K))
+    s = (2.0 ** -rng.integers(4, 9, (N, K // 128))).astype(np.float32)      # exact in fp16
+    z = rng.integers(0, 16, (N, K // 128)).astype(np.float32)
+    gidx = np.arange(K) // 128
+    W = ((q - z[:, gidx]) * s[:, gidx]).astype(np.float16)                  # exact
+    assert np.array_equal(O.quantize_intweight(W, s, z), q)
+
+
+def test_quantize_intweight_rounds_half_to_even():
+    W = np.array([[0.5, 1.5, 2.5, 3.5, -0.5, 4.5] + [0.0] * 58], np.float16)
+    q = O.quantize_intweight(W, np.ones((1, 1), np.float16), np.zeros((1, 1), np.float16), group_size=64)
+    assert q[0, :6].tolist() == [0, 2, 2, 4, 0, 4]
+
+
+def test_quantize_intweight_matches_torch_16bit_ops():
+    """The per-op roundings, cross-checked against torch's fp16 / bf16 tensor
+    arithmetic running the from_linear expression (qmodule.py:296-305)."""
+    import torch
+    rng = np.random.default_rng(6)
+    N, K, gs = 48, 384, 64
+    W32 = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    s32 = rng.uniform(0.002, 0.02, (N, K // gs)).astype(np.float32)
+    z32 = rng.integers(0, 16, (N, K // gs)).astype(np.float32)
+    gidx = torch.arange(K) // gs
+    for tdt, odt in ((torch.float16, np.float16), (torch.bfloat16, "bf16")):
+        Wt, st, zt = (torch.from_numpy(a).to(tdt) for a in (W32, s32, z32))
+        ref = torch.round((Wt + (zt * st)[:, gidx]) / st[:, gidx]).to(torch.int32).numpy()
+        got = O.quantize_intweight(Wt.float().numpy(), st.float().numpy(), zt.float().numpy(), gs, dtype=odt)
+        assert np.array_equal(got, ref), tdt
