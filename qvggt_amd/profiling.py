@@ -5,6 +5,8 @@
     python qvggt_amd/profiling.py aggregator [--frames S] [--w8a8]
     python qvggt_amd/profiling.py attention [--frames S] [--global] [--reps R]
     python qvggt_amd/profiling.py camera [--frames S] [--reps R] [--graph]
+    python qvggt_amd/profiling.py dense M K N [--bias]
+    python qvggt_amd/profiling.py sdpa [--frames S] [--global]
 
 ``copy`` launches one elementwise kernel that reads 512 MiB and writes
 512 MiB, three times: the FETCH_SIZE / WRITE_SIZE it reports per dispatch
@@ -106,6 +108,58 @@ def _camera(S, reps, graph):
     print(f"camera: S={S} graph={graph}, {reps} forwards, {ms:.3f} ms per forward", flush=True)
 
 
+def _replay_us(fn, reps=20, rounds=5):
+    import time
+
+    import torch
+    a = torch.randn(4096, 4096, device="cuda", dtype=torch.float16)
+    t0 = time.time()
+    while time.time() - t0 < 1.0:
+        a @ a
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(rounds):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * rounds)
+
+
+def _dense(M, K, N, bias):
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, K, generator=g).half().to(dev)
+    w = torch.randn(N, K, generator=g).half().to(dev)
+    b = torch.randn(N, generator=g).half().to(dev)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    fn = (lambda: torch.addmm(b, x, w.t(), out=out)) if bias else (lambda: torch.mm(x, w.t(), out=out))
+    us = _replay_us(fn)
+    print(f"dense fp16 {'addmm' if bias else 'mm'}: M={M} K={K} N={N}, {us:.1f} us, "
+          f"{2 * M * N * K / us / 1e6:.1f} TFLOP/s", flush=True)
+
+
+def _sdpa(S, glob):
+    import torch
+    import torch.nn.functional as F
+    dev = torch.device("cuda:0")
+    B, L = (1, S * 1374) if glob else (S, 1374)
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, 16, L, 64, generator=g).half().to(dev) for _ in range(3))
+    us = _replay_us(lambda: F.scaled_dot_product_attention(q, k, v), reps=2 if glob else 10, rounds=3)
+    print(f"sdpa fp16: S={S} global={glob} (B={B}, L={L}, 16 heads x 64), {us:.1f} us, "
+          f"{4 * B * 16 * L * L * 64 / us / 1e6:.1f} TFLOP/s", flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -127,6 +181,14 @@ def main(argv=None):
     c.add_argument("--frames", type=int, default=32)
     c.add_argument("--reps", type=int, default=10)
     c.add_argument("--graph", action="store_true")
+    d = sub.add_parser("dense")
+    d.add_argument("M", type=int)
+    d.add_argument("K", type=int)
+    d.add_argument("N", type=int)
+    d.add_argument("--bias", action="store_true")
+    q = sub.add_parser("sdpa")
+    q.add_argument("--frames", type=int, default=8)
+    q.add_argument("--global", dest="glob", action="store_true")
     args = ap.parse_args(argv)
     if args.mode == "copy":
         _copy()
@@ -136,6 +198,10 @@ def main(argv=None):
         _attention(args.frames, args.glob, args.reps)
     elif args.mode == "camera":
         _camera(args.frames, args.reps, args.graph)
+    elif args.mode == "dense":
+        _dense(args.M, args.K, args.N, args.bias)
+    elif args.mode == "sdpa":
+        _sdpa(args.frames, args.glob)
     else:
         _aggregator(args.frames, args.w8a8)
 
