@@ -210,17 +210,20 @@ def kernel_suite(dev):
     us = _time_graph(lambda i: E.qknorm_rope2d(qkv[i % 4], pos, ct, st, 16, gq, bq, gq, bq), 8)
     r["qknorm_rope2d_S32"] = {"us": round(us, 1), "GB/s": round(8 * M * D / us / 1e3, 1)}
     del qkv, xs
-    # GEMV: camera/register tokens, 1024 -> 3072, rotating 600 weight sets (~1 GiB)
-    nw = 600
-    _, qw0, scl, szs = synthetic_w4(0, 1024, 3072, seed=0, dev=dev)
-    qw = [qw0.clone() for _ in range(nw)]
-    for m in (1, 8, 16):
-        x = torch.randn(m, 1024, **f16)
-        out = torch.empty(m, 3072, **f16)
-        us = _time_graph(lambda i: E.w4a16_linear(x, qw[i % nw], scl, szs, out=out), nw)
-        byts = 3072 * 1024 / 2 + 4 * 8 * 3072 + 2 * m * 1024 + 2 * m * 3072
-        r[f"gemv_M{m}_1024x3072"] = {"us": round(us, 2), "GB/s": round(byts / us / 1e3, 1)}
-    del qw
+    # skinny M (the GEMV entry): aggregator qkv 1024 -> 3072 and the camera-head
+    # fc1 / fc2 shapes, weights cold (rotating sets of ~1 GiB)
+    for K, N in ((1024, 3072), (2048, 8192), (8192, 2048)):
+        wbytes = N * K // 2
+        nw = max(16, (1 << 30) // wbytes)
+        _, qw0, scl, szs = synthetic_w4(0, K, N, seed=0, dev=dev)
+        qw = [qw0.clone() for _ in range(nw)]
+        for m in (1, 8, 32):
+            x = torch.randn(m, K, **f16)
+            out = torch.empty(m, N, **f16)
+            us = _time_graph(lambda i: E.w4a16_linear(x, qw[i % nw], scl, szs, out=out), nw)
+            byts = wbytes + 4 * (K // 128) * N + 2 * m * K + 2 * m * N
+            r[f"w4_skinny_M{m}_{K}x{N}"] = {"us": round(us, 2), "GB/s": round(byts / us / 1e3, 1)}
+        del qw
     # attention (MFMA-bound): frame S=8 and global S=32
     for name, Bq, L in (("attention_frame_S8", 8, 1374), ("attention_global_S32", 1, 32 * 1374)):
         qk = torch.randn(Bq * L, 3, 16, 64, **f16)
@@ -236,6 +239,25 @@ def kernel_suite(dev):
     us = _time_graph(lambda i: E.w8a8_gemm_forward_cuda(a, w, ws_, as_, o), 10)
     r["w8a8_fc1_M10992"] = {"us": round(us, 1), "TOPS": round(2.0 * 10992 * 4096 * 1024 / us / 1e6, 1)}
     return r
+
+
+def camera_head_ms(dev, S=32, reps=50):
+    """VGGT camera head (W4 trunk, 4 iterations) on S pose tokens, replayed from
+    one HIP graph: wall ms per forward."""
+    import torch
+
+    from qvggt_amd.camera_head import CameraHead, GraphedCameraHead
+
+    head = GraphedCameraHead(CameraHead.random(seed=0, device=dev), S)
+    t = torch.randn(S, 2048, device=dev).half()
+    for _ in range(5):
+        head(t)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        head(t)
+    torch.cuda.synchronize()
+    return {"S": S, "ms_per_forward": round((time.perf_counter() - t0) * 1e3 / reps, 3), "graph": True}
 
 
 def profiled_traffic():
@@ -261,6 +283,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-aggregator", action="store_true")
     ap.add_argument("--no-kernel-suite", action="store_true")
+    ap.add_argument("--no-camera-head", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -334,6 +357,11 @@ def main():
         log(f"[bench] aggregator S={agg['S']}: {agg['ms_per_forward']:.1f} ms/forward, "
             f"{agg['frames_per_s']:.1f} frames/s")
 
+    cam = None
+    if not args.no_camera_head:
+        cam = camera_head_ms(dev)
+        log(f"[bench] camera head S={cam['S']} (HIP graph): {cam['ms_per_forward']:.3f} ms/forward")
+
     cpu, err = None, None
     if not args.no_cpu_baseline:
         cpu, err = cpu_baseline_mlp(x, w1, b1, w2, b2, y)
@@ -361,6 +389,7 @@ def main():
                    "fc1_us": round(fc1_ms * 1e3, 2), "fc2_us": round(fc2_ms * 1e3, 2),
                    "rel_err_vs_oracle": err},
         "aggregator": agg,
+        "camera_head": cam,
         "kernels": kernels,
         "roofline": {"bound": "mfma", "achieved": round(fc1_tflops, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fc1_tflops / PEAK_FP16_TFLOPS, 4),

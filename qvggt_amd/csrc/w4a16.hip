@@ -264,32 +264,88 @@ __global__ __launch_bounds__(1024) void w4a16_skinny_kernel(
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[j][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  for (int kt = wave; kt < KT; kt += nwaves) {
-    uint4 wq[NB];
-    uint32_t sj[NB], zj[NB];
+  // One 128-k group per step.  The next step's weights and group scales (HBM)
+  // are loaded before this step's dequant + MFMAs, and so are its activations
+  // (L2), where the 128-VGPR budget of a 1024-thread group allows (weights for
+  // MB * NB < 8, activations for MB * NB <= 2), so a wave with several groups
+  // (K > 128 * waves) keeps the next group in flight.
+  constexpr bool PREW = MB * NB < 8, PREX = MB * NB <= 2;
+  uint4 wq[NB], xb[MB][4];
+  uint32_t sj[NB], zj[NB];
+  auto load_w = [&](int k, uint4 (&w)[NB], uint32_t (&sv)[NB], uint32_t (&zv)[NB]) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int n = n0 + 16 * j + li;
-      wq[j] = *reinterpret_cast<const uint4*>(qw + qw_chunk_u32(n, kt, g, K));
-      sj[j] = scales[(size_t)kt * N + n];
-      zj[j] = zeros[(size_t)kt * N + n];
+      w[j] = *reinterpret_cast<const uint4*>(qw + qw_chunk_u32(n, k, g, K));
+      sv[j] = scales[(size_t)k * N + n];
+      zv[j] = zeros[(size_t)k * N + n];
     }
-    uint4 xb[MB][4];
+  };
+  auto load_x = [&](int k, uint4 (&xv)[MB][4]) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) xb[mb][t] = buf_load16(rsX, x_voff, mb * 16 * K2 + kt * 256 + t * 16);
+      for (int t = 0; t < 4; ++t) xv[mb][t] = buf_load16(rsX, x_voff, mb * 16 * K2 + k * 256 + t * 16);
+  };
+  if constexpr (!PREW) {
+    for (int kt = wave; kt < KT; kt += nwaves) {
+      load_w(kt, wq, sj, zj);
+      load_x(kt, xb);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      uint4 wf[4];
-      wf[0] = dq_frag<BF16, 0>(wq[j], sj[j], zj[j]);
-      wf[1] = dq_frag<BF16, 1>(wq[j], sj[j], zj[j]);
-      wf[2] = dq_frag<BF16, 2>(wq[j], sj[j], zj[j]);
-      wf[3] = dq_frag<BF16, 3>(wq[j], sj[j], zj[j]);
+      for (int j = 0; j < NB; ++j) {
+        uint4 wf[4];
+        wf[0] = dq_frag<BF16, 0>(wq[j], sj[j], zj[j]);
+        wf[1] = dq_frag<BF16, 1>(wq[j], sj[j], zj[j]);
+        wf[2] = dq_frag<BF16, 2>(wq[j], sj[j], zj[j]);
+        wf[3] = dq_frag<BF16, 3>(wq[j], sj[j], zj[j]);
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[j][mb] = mfma16<BF16>(wf[t], xb[mb][t], acc[j][mb]);
+          for (int mb = 0; mb < MB; ++mb) acc[j][mb] = mfma16<BF16>(wf[t], xb[mb][t], acc[j][mb]);
+      }
+    }
+  } else {
+    int kt = wave;
+    if (kt < KT) {
+      load_w(kt, wq, sj, zj);
+      load_x(kt, xb);
+    }
+    for (; kt < KT; kt += nwaves) {
+      const int kn = kt + nwaves;
+      uint4 wq2[NB], xb2[MB][4];
+      uint32_t sj2[NB], zj2[NB];
+      if (kn < KT) {
+        load_w(kn, wq2, sj2, zj2);
+        if constexpr (PREX) load_x(kn, xb2);
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        uint4 wf[4];
+        wf[0] = dq_frag<BF16, 0>(wq[j], sj[j], zj[j]);
+        wf[1] = dq_frag<BF16, 1>(wq[j], sj[j], zj[j]);
+        wf[2] = dq_frag<BF16, 2>(wq[j], sj[j], zj[j]);
+        wf[3] = dq_frag<BF16, 3>(wq[j], sj[j], zj[j]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[j][mb] = mfma16<BF16>(wf[t], xb[mb][t], acc[j][mb]);
+      }
+      if (kn < KT) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          wq[j] = wq2[j];
+          sj[j] = sj2[j];
+          zj[j] = zj2[j];
+        }
+        if constexpr (PREX) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xb[mb][t] = xb2[mb][t];
+        } else {
+          load_x(kn, xb);
+        }
+      }
     }
   }
   // Cross-wave sums, one 16-channel block at a time through the same LDS.
