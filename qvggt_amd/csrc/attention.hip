@@ -14,7 +14,9 @@
 // The softmax is trimmed to what the MFMAs cannot hide: key masking only on
 // the last (partial) tile, one fma + exp2 per score, row sums by v_dot2 on
 // the fp16 P values, and a lazy rescale -- the reference maximum moves only
-// when a tile exceeds it by 2^8, so most tiles skip the O *= alpha pass.
+// when a tile exceeds it by 2^8, so most tiles skip the O *= alpha pass, and
+// the tile maximum itself is only computed when a lane's tile sum says some
+// P may have exceeded 2^8.
 // Layouts:
 //  * S^T layout: lane (h = lane/32, q = lane%32) holds, for key block kb,
 //    keys 32kb + 8*(r/4) + 4h + r%4 (r = 0..15) of query q.  A query's 64
@@ -37,6 +39,7 @@ constexpr int ATT_BQ = 4 * ATT_QW;         // queries per workgroup
 constexpr int ATT_BK = 64;                 // keys per tile
 
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units: P <= 256 between rescales
+constexpr float P_SUM_LIMIT = 256.0f;  // 2^RESCALE_SLACK: a lane's tile sum above it may hide a P above it
 
 __device__ __forceinline__ int fk(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
@@ -200,42 +203,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int r = 0; r < 16; ++r)
             if (key0 + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[qb][kb][r] = -INFINITY;
       }
-      // ---- tile maximum of this query (both lane halves hold 32 keys each)
-      float mx = sc[qb][0][0];
+      // ---- P = 2^(s * scale_log2 - m_use) in fp16 against the current
+      // reference, with this tile's partial row sum t (v_dot2 on the fp16
+      // values).  The tile maximum is only needed when some P could exceed
+      // 2^RESCALE_SLACK, and every such P makes t exceed it too (P >= 0), so
+      // the maximum is computed only for waves where some lane's t does; a
+      // non-finite t (the first tile, where m_use = -inf) lands there as well.
+      float t = 0.f;
+      auto make_p = [&]() {
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[qb][0][r]);
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[qb][1][r]);
-      mx = half_max(mx) * scale_log2;
-      // ---- lazy rescale: wave-uniform branch, taken when any query's tile
-      // maximum exceeds its reference by more than the slack
-      const bool need = mx > m_use[qb] + RESCALE_SLACK;
-      if (__builtin_amdgcn_ballot_w64(need)) {
-        const float m_new = need ? mx : m_use[qb];
-        const float alpha = __builtin_amdgcn_exp2f(m_use[qb] - m_new);  // 0 on the first tile, 1 if !need
-        m_use[qb] = m_new;
-        l_run[qb] *= alpha;
+          for (int pp = 0; pp < 2; ++pp) {
+            uint32_t w[4];
 #pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
-      }
-      // ---- P = 2^(s * scale_log2 - m_use) in fp16, row sums from the fp16 values
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int pp = 0; pp < 2; ++pp) {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][8 * pp + 2 * e], scale_log2, -m_use[qb]));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][8 * pp + 2 * e + 1], scale_log2, -m_use[qb]));
-            const f16x2 ph = {(_Float16)p0, (_Float16)p1};
-            l_run[qb] = __builtin_amdgcn_fdot2(ph, ones, l_run[qb], false);
-            w[e] = __builtin_bit_cast(uint32_t, ph);
+            for (int e = 0; e < 4; ++e) {
+              const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][8 * pp + 2 * e], scale_log2, -m_use[qb]));
+              const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][8 * pp + 2 * e + 1], scale_log2, -m_use[qb]));
+              const f16x2 ph = {(_Float16)p0, (_Float16)p1};
+              t = __builtin_amdgcn_fdot2(ph, ones, t, false);
+              w[e] = __builtin_bit_cast(uint32_t, ph);
+            }
+            pf[qb][2 * kb + pp] = make_uint4(w[0], w[1], w[2], w[3]);
           }
-          pf[qb][2 * kb + pp] = make_uint4(w[0], w[1], w[2], w[3]);
+      };
+      make_p();
+      if (__builtin_amdgcn_ballot_w64(!(t <= P_SUM_LIMIT))) {
+        // ---- tile maximum of this query (both lane halves hold 32 keys each)
+        float mx = sc[qb][0][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[qb][0][r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[qb][1][r]);
+        mx = half_max(mx) * scale_log2;
+        // ---- lazy rescale: the reference moves when the tile maximum exceeds
+        // it by more than the slack; then P is recomputed against it
+        const bool need = mx > m_use[qb] + RESCALE_SLACK;
+        if (__builtin_amdgcn_ballot_w64(need)) {
+          const float m_new = need ? mx : m_use[qb];
+          const float alpha = __builtin_amdgcn_exp2f(m_use[qb] - m_new);  // 0 on the first tile, 1 if !need
+          m_use[qb] = m_new;
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+          t = 0.f;
+          make_p();
         }
+      }
+      l_run[qb] += t;
     }
     // ---- O^T += V^T P^T: each V^T fragment (16 contiguous bytes) feeds both query blocks
     const uint8_t* vb = v_lds[buf];
