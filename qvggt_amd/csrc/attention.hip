@@ -12,11 +12,12 @@
 // both blocks), the online softmax in registers, and O^T += V^T P^T (16 more
 // MFMAs, each V^T fragment again feeding both blocks).
 // The softmax is trimmed to what the MFMAs cannot hide: key masking only on
-// the last (partial) tile, one fma + exp2 per score, row sums by v_dot2 on
-// the fp16 P values, and a lazy rescale -- the reference maximum moves only
-// when a tile exceeds it by 2^8, so most tiles skip the O *= alpha pass, and
-// the tile maximum itself is only computed when a lane's tile sum says some
-// P may have exceeded 2^8.
+// the last (partial) tile; Q pre-scaled by scale * log2(e) and the score
+// accumulators started at -m (the running reference), so P = 2^S takes one
+// exp2 per score and nothing else; row sums by v_dot2 on the fp16 P values;
+// and a lazy rescale -- the reference moves only when a tile exceeds it by
+// 2^8, so most tiles skip the O *= alpha pass, and the tile maximum itself is
+// only computed when a lane's tile sum says some P may have exceeded 2^8.
 // Layouts:
 //  * S^T layout: lane (h = lane/32, q = lane%32) holds, for key block kb,
 //    keys 32kb + 8*(r/4) + 4h + r%4 (r = 0..15) of query q.  A query's 64
@@ -108,7 +109,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int qc = qi[qb] < L ? qi[qb] : L - 1;
     const uint16_t* qp = q + (tok0 + qc) * q_ts + (long)head * 64;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[qb][s] = *reinterpret_cast<const uint4*>(qp + 16 * s + 8 * h);
+    for (int s = 0; s < 4; ++s) {
+      // pre-scaled by scale * log2(e) (one fp16 rounding), so the MFMA yields
+      // scores in log2 units and the softmax needs no per-score multiply
+      const uint4 raw = *reinterpret_cast<const uint4*>(qp + 16 * s + 8 * h);
+      const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+      uint32_t sw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 hv = __builtin_bit_cast(f16x2, rw[e]);
+        const f16x2 sv = {(_Float16)((float)hv[0] * scale_log2), (_Float16)((float)hv[1] * scale_log2)};
+        sw[e] = __builtin_bit_cast(uint32_t, sv);
+      }
+      qf[qb][s] = make_uint4(sw[0], sw[1], sw[2], sw[3]);
+    }
   }
 
   // ---- K tile DMA: 8 x 1 KB per tile, 2 per wave; lane L lands at key
@@ -166,6 +180,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // when a tile's maximum exceeds it by more than RESCALE_SLACK, so P values
   // stay <= 2^RESCALE_SLACK and most tiles skip the O rescale.
   float m_use[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  // base: the reference the score accumulators start from (S' = S - base,
+  // the MFMA's C input), equal to m_use after the first tile, so P = 2^S'
+  // needs one exp2 per score and nothing else
+  float base[2] = {0.f, 0.f};
   const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
   auto tile = [&](int j, bool mask) {
@@ -187,9 +205,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const uint4 kf = *reinterpret_cast<const uint4*>(kb_lds + row * 128 + ((c ^ fk(row)) * 16));
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
-          sc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf),
-                                                             __builtin_bit_cast(f16x8, qf[qb][st]),
-                                                             st == 0 ? f32x16{} : sc[qb][kb], 0, 0, 0);
+          sc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              __builtin_bit_cast(f16x8, kf), __builtin_bit_cast(f16x8, qf[qb][st]),
+              st == 0 ? f32x16{} - base[qb] : sc[qb][kb], 0, 0, 0);
       }
     }
     uint4 pf[2][4];
@@ -203,14 +221,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int r = 0; r < 16; ++r)
             if (key0 + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[qb][kb][r] = -INFINITY;
       }
-      // ---- P = 2^(s * scale_log2 - m_use) in fp16 against the current
-      // reference, with this tile's partial row sum t (v_dot2 on the fp16
-      // values).  The tile maximum is only needed when some P could exceed
-      // 2^RESCALE_SLACK, and every such P makes t exceed it too (P >= 0), so
-      // the maximum is computed only for waves where some lane's t does; a
-      // non-finite t (the first tile, where m_use = -inf) lands there as well.
+      // ---- P = 2^S' = 2^(S - m_use) in fp16 against the current reference,
+      // with this tile's partial row sum t (v_dot2 on the fp16 values).  The
+      // tile maximum is only needed when some P could exceed 2^RESCALE_SLACK,
+      // and every such P makes t exceed it too (P >= 0), so the maximum is
+      // computed only for waves where some lane's t does, and on the first
+      // tile (no reference yet).
       float t = 0.f;
-      auto make_p = [&]() {
+      auto make_p = [&](bool shift, float off) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -218,8 +236,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             uint32_t w[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][8 * pp + 2 * e], scale_log2, -m_use[qb]));
-              const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][kb][8 * pp + 2 * e + 1], scale_log2, -m_use[qb]));
+              const float s0 = sc[qb][kb][8 * pp + 2 * e], s1 = sc[qb][kb][8 * pp + 2 * e + 1];
+              const float p0 = __builtin_amdgcn_exp2f(shift ? s0 + off : s0);
+              const float p1 = __builtin_amdgcn_exp2f(shift ? s1 + off : s1);
               const f16x2 ph = {(_Float16)p0, (_Float16)p1};
               t = __builtin_amdgcn_fdot2(ph, ones, t, false);
               w[e] = __builtin_bit_cast(uint32_t, ph);
@@ -227,15 +246,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             pf[qb][2 * kb + pp] = make_uint4(w[0], w[1], w[2], w[3]);
           }
       };
-      make_p();
-      if (__builtin_amdgcn_ballot_w64(!(t <= P_SUM_LIMIT))) {
+      make_p(false, 0.f);
+      if (__builtin_amdgcn_ballot_w64(!(t <= P_SUM_LIMIT) || m_use[qb] == -INFINITY)) {
         // ---- tile maximum of this query (both lane halves hold 32 keys each)
         float mx = sc[qb][0][0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[qb][0][r]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[qb][1][r]);
-        mx = half_max(mx) * scale_log2;
+        mx = half_max(mx) + base[qb];
         // ---- lazy rescale: the reference moves when the tile maximum exceeds
         // it by more than the slack; then P is recomputed against it
         const bool need = mx > m_use[qb] + RESCALE_SLACK;
@@ -249,8 +268,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
           t = 0.f;
-          make_p();
+          make_p(true, base[qb] - m_new);
         }
+        base[qb] = m_use[qb];
       }
       l_run[qb] += t;
     }
