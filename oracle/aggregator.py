@@ -27,7 +27,7 @@ from .attention import attention_ref
 DIM, HEADS, HD = 1024, 16, 64
 
 
-def _ln(x, g, b, eps=1e-5):
+def _ln(x, g, b, eps=1e-6):
     x = np.asarray(x, np.float64)
     m = x.mean(-1, keepdims=True)
     v = ((x - m) ** 2).mean(-1, keepdims=True)

@@ -35,7 +35,7 @@ import torch.nn.functional as F
 
 from . import awq_inference_engine as E
 from ._lib import QV_EPI_BIAS, QV_EPI_BIAS_GELU
-from .aggregator import BLOCK_LN_EPS, LayerScale, Mlp, _linear, quantize_w4
+from .aggregator import LayerScale, Mlp, _linear, quantize_w4
 
 DIM = 2048
 HEADS = 16
@@ -43,7 +43,7 @@ HEAD_DIM = DIM // HEADS      # 128
 MLP_DIM = 4 * DIM
 TRUNK_DEPTH = 4
 POSE_DIM = 9                 # absT (3) + quaternion (4) + FoV (2)
-LN_EPS = BLOCK_LN_EPS        # token_norm, trunk_norm, trunk blocks
+LN_EPS = 1e-5               # token_norm, trunk_norm, trunk blocks (torch's default)
 ADALN_EPS = 1e-6
 
 

@@ -42,7 +42,7 @@ def _params(rng, zero_out=False):
 
 def _ln64(x, g, b):
     m = x.mean(-1, keepdims=True)
-    return (x - m) / np.sqrt(x.var(-1, keepdims=True) + 1e-5) * g + b
+    return (x - m) / np.sqrt(x.var(-1, keepdims=True) + 1e-6) * g + b
 
 
 def test_zero_projections_leave_layerscaled_biases():
