@@ -87,8 +87,8 @@ __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict_
   const int base = 32 * half + 8 * sub;
   const uint16_t* s = src + (size_t)tok * src_tok + (size_t)part * H * 64 + (size_t)head * 64 + base;
   uint16_t* d = dst + (size_t)tok * dst_tok + (size_t)part * dst_part + (size_t)head * 64 + base;
-  const f16x8 a = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(s));
-  const f16x8 b = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(s + 16));
+  const f16x8 a = __builtin_bit_cast(f16x8, ld_stream16(s));
+  const f16x8 b = __builtin_bit_cast(f16x8, ld_stream16(s + 16));
   const float4* cp = reinterpret_cast<const float4*>(cos_t + (size_t)p * 16 + 8 * sub);
   const float4* sp = reinterpret_cast<const float4*>(sin_t + (size_t)p * 16 + 8 * sub);
   const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
@@ -101,8 +101,8 @@ __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict_
     oa[e] = (_Float16)(xa * cs[e] - xb * sn[e]);
     ob[e] = (_Float16)(xb * cs[e] + xa * sn[e]);
   }
-  *reinterpret_cast<uint4*>(d) = __builtin_bit_cast(uint4, oa);
-  *reinterpret_cast<uint4*>(d + 16) = __builtin_bit_cast(uint4, ob);
+  st_stream16(d, __builtin_bit_cast(uint4, oa));
+  st_stream16(d + 16, __builtin_bit_cast(uint4, ob));
 }
 
 // VGGT attention prologue, fused: per-head LayerNorm of q and k (qk-norm,
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
   uint16_t* row = qkv + (size_t)tok * tok_stride + (size_t)part * H * 64 + (size_t)head * 64;
   float x[8];
   {
-    const f16x8 v = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(row)[j]);
+    const f16x8 v = __builtin_bit_cast(f16x8, ld_stream16(row + 8 * j));
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = (float)v[e];
   }
@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
     const float v = lo ? x[e] * cs[e] - other * sn[e] : x[e] * cs[e] + other * sn[e];
     o[e] = __builtin_bit_cast(_Float16, from_f32<false>(v));
   }
-  if (live) reinterpret_cast<uint4*>(row)[j] = __builtin_bit_cast(uint4, o);
+  if (live) st_stream16(row + 8 * j, __builtin_bit_cast(uint4, o));
 }
 
 }  // namespace qv
