@@ -110,14 +110,15 @@ def cpu_baseline_mlp(x, w1, b1, w2, b2, y, M_sample: int = 2748, reps: int = 5):
                        f"CPU: {cpu_model()}"), err
 
 
-def aggregator_fps(dev, S: int = 32, reps: int = 3):
-    """VGGT-1B aggregator (W4A16 g128 AA blocks, fp16 DINOv2-L/14-reg patch embed,
-    seeded random-init weights) on S synthetic 518x518 frames U[0,1]: frames/s."""
+def aggregator_fps(dev, S: int = 32, reps: int = 3, w8a8: bool = False):
+    """VGGT-1B aggregator (W4A16 g128 or W8A8 AA blocks, fp16 DINOv2-L/14-reg
+    patch embed, seeded random-init weights) on S synthetic 518x518 frames
+    U[0,1]: frames/s."""
     import torch
 
     from qvggt_amd import aggregator as AG
 
-    agg = AG.Aggregator.random(w8a8=False, seed=0, device=dev)
+    agg = AG.Aggregator.random(w8a8=w8a8, seed=0, device=dev)
     g = torch.Generator(device=dev).manual_seed(1)
     img = torch.rand(S, 3, AG.IMG, AG.IMG, generator=g, device=dev).half()
     agg(img)
@@ -134,7 +135,8 @@ def aggregator_fps(dev, S: int = 32, reps: int = 3):
     del agg, out
     torch.cuda.empty_cache()
     return {"S": S, "frames_per_s": round(S / ms * 1e3, 2), "ms_per_forward": round(ms, 2), "reps": reps,
-            "variant": "W4A16 g128 frame/global blocks (24+24), fp16 DINOv2-L/14-reg patch embed",
+            "variant": ("W8A8 (per-token int8 activations, per-channel int8 weights)" if w8a8 else "W4A16 g128")
+                       + " frame/global blocks (24+24), fp16 DINOv2-L/14-reg patch embed",
             "data": "seeded random-init weights, images U[0,1]", "finite": ok,
             "flop_per_forward": 2.816e14}
 
@@ -238,6 +240,24 @@ def kernel_suite(dev):
     o = torch.empty(10992, 4096, **f16)
     us = _time_graph(lambda i: E.w8a8_gemm_forward_cuda(a, w, ws_, as_, o), 10)
     r["w8a8_fc1_M10992"] = {"us": round(us, 1), "TOPS": round(2.0 * 10992 * 4096 * 1024 / us / 1e6, 1)}
+    # W8A8 MLP pair (W8A8 variant): fc1 + bias, GELU + per-token
+    # quant of the hidden activations, fc2 + bias
+    x8 = torch.randint(-128, 128, (10992, 1024), dtype=torch.int8, device=dev)
+    s8 = torch.rand(10992, **f16) * 0.01
+    w2 = torch.randint(-128, 128, (1024, 4096), dtype=torch.int8, device=dev)
+    ws2 = torch.rand(1024, **f16) * 0.01
+    b1, b2 = torch.zeros(4096, **f16), torch.zeros(1024, **f16)
+    hq = torch.empty(10992, 4096, dtype=torch.int8, device=dev)
+    hs, ht = torch.empty(10992, **f16), torch.empty(10992, 4096, **f16)
+    y8 = torch.empty(10992, 1024, **f16)
+
+    def w8_pair(i):
+        E.w8a8_gemm_fuse_bias_forward_cuda(x8, w, ws_, s8, o, b1)
+        E.gelu_and_quant(hq, o, hs, ht)
+        E.w8a8_gemm_fuse_bias_forward_cuda(hq, w2, ws2, hs, y8, b2)
+
+    us = _time_graph(w8_pair, 5)
+    r["w8a8_mlp_pair_M10992"] = {"us": round(us, 1), "TOPS": round(2 * 2.0 * 10992 * 4096 * 1024 / us / 1e6, 1)}
     return r
 
 
@@ -351,11 +371,14 @@ def main():
         for k, v in kernels.items():
             log(f"[bench] {k}: {v}")
 
-    agg = None
+    agg = agg8 = None
     if not args.no_aggregator:
         agg = aggregator_fps(dev)
         log(f"[bench] aggregator S={agg['S']}: {agg['ms_per_forward']:.1f} ms/forward, "
             f"{agg['frames_per_s']:.1f} frames/s")
+        agg8 = aggregator_fps(dev, w8a8=True)
+        log(f"[bench] aggregator W8A8 S={agg8['S']}: {agg8['ms_per_forward']:.1f} ms/forward, "
+            f"{agg8['frames_per_s']:.1f} frames/s")
 
     cam = None
     if not args.no_camera_head:
@@ -389,6 +412,7 @@ def main():
                    "fc1_us": round(fc1_ms * 1e3, 2), "fc2_us": round(fc2_ms * 1e3, 2),
                    "rel_err_vs_oracle": err},
         "aggregator": agg,
+        "aggregator_w8a8": agg8,
         "camera_head": cam,
         "kernels": kernels,
         "roofline": {"bound": "mfma", "achieved": round(fc1_tflops, 2), "peak": PEAK_FP16_TFLOPS,
