@@ -64,45 +64,58 @@ __global__ __launch_bounds__(256) void rope_with_pos_kernel(
   }
 }
 
-// VGGT 2-D RoPE.  One thread per (token, part in {q,k}, head, half, sub):
-// it owns dims base..base+7 and their partners base+16..base+23 with
-// base = 32*half + 8*sub, frequency indices 8*sub .. 8*sub+7.
+// VGGT 2-D RoPE.  One thread per (token, part in {q,k}, head group, half,
+// sub): it owns dims base..base+7 and their partners base+16..base+23 with
+// base = 32*half + 8*sub, frequency indices 8*sub .. 8*sub+7, in NH heads
+// h0, h0 + H/NH, ... that share one (position, frequency) pair, so each
+// cos / sin table read serves NH heads.  Consecutive threads cover
+// consecutive heads, so every load and store instruction of a wave moves
+// whole 128-byte head rows.
+template <int NH>
 __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                      const int* __restrict__ pos, const float* __restrict__ cos_t,
                                                      const float* __restrict__ sin_t, int P, int T, int H,
                                                      long src_tok, long dst_tok, long dst_part) {
   const long gid = (long)blockIdx.x * 256 + threadIdx.x;
-  const long per_tok = 2L * H * 4;
+  const int HG = H / NH;
+  const long per_tok = 2L * HG * 4;
   if (gid >= (long)T * per_tok) return;
   const int tok = (int)(gid / per_tok);
   int r = (int)(gid % per_tok);
   const int sub = r & 1;
   const int half = (r >> 1) & 1;
-  const int head = (r >> 2) % H;
-  const int part = (r >> 2) / H;
+  const int h0 = (r >> 2) % HG;
+  const int part = (r >> 2) / HG;
   // positions outside the table are clamped (never read out of bounds);
   // callers keep them in [0, P)
   int p = pos[2 * tok + half];
   p = p < 0 ? 0 : (p >= P ? P - 1 : p);
   const int base = 32 * half + 8 * sub;
-  const uint16_t* s = src + (size_t)tok * src_tok + (size_t)part * H * 64 + (size_t)head * 64 + base;
-  uint16_t* d = dst + (size_t)tok * dst_tok + (size_t)part * dst_part + (size_t)head * 64 + base;
-  const f16x8 a = __builtin_bit_cast(f16x8, ld_stream16(s));
-  const f16x8 b = __builtin_bit_cast(f16x8, ld_stream16(s + 16));
   const float4* cp = reinterpret_cast<const float4*>(cos_t + (size_t)p * 16 + 8 * sub);
   const float4* sp = reinterpret_cast<const float4*>(sin_t + (size_t)p * 16 + 8 * sub);
   const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
   const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
   const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-  f16x8 oa, ob;
+  f16x8 a[NH], b[NH];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float xa = (float)a[e], xb = (float)b[e];
-    oa[e] = (_Float16)(xa * cs[e] - xb * sn[e]);
-    ob[e] = (_Float16)(xb * cs[e] + xa * sn[e]);
+  for (int k = 0; k < NH; ++k) {
+    const uint16_t* s = src + (size_t)tok * src_tok + (size_t)part * H * 64 + (size_t)(h0 + k * HG) * 64 + base;
+    a[k] = __builtin_bit_cast(f16x8, ld_stream16(s));
+    b[k] = __builtin_bit_cast(f16x8, ld_stream16(s + 16));
   }
-  st_stream16(d, __builtin_bit_cast(uint4, oa));
-  st_stream16(d + 16, __builtin_bit_cast(uint4, ob));
+#pragma unroll
+  for (int k = 0; k < NH; ++k) {
+    f16x8 oa, ob;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float xa = (float)a[k][e], xb = (float)b[k][e];
+      oa[e] = (_Float16)(xa * cs[e] - xb * sn[e]);
+      ob[e] = (_Float16)(xb * cs[e] + xa * sn[e]);
+    }
+    uint16_t* d = dst + (size_t)tok * dst_tok + (size_t)part * dst_part + (size_t)(h0 + k * HG) * 64 + base;
+    st_stream16(d, __builtin_bit_cast(uint4, oa));
+    st_stream16(d + 16, __builtin_bit_cast(uint4, ob));
+  }
 }
 
 // VGGT attention prologue, fused: per-head LayerNorm of q and k (qk-norm,
@@ -255,10 +268,23 @@ extern "C" int qv_rope2d(const void* qkv, void* out, const int32_t* positions, c
                    ((uintptr_t)qkv % 16) == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)cos_table % 16) == 0 &&
                    ((uintptr_t)sin_table % 16) == 0,
                "rope2d needs 16-byte aligned rows and tables");
-  const long total = T * 2 * H * 4;
+  // two heads per thread measured 5 % faster than one and 1.5 % faster than
+  // four at S = 32 (QVGGT_ROPE_NH=1|2|4 overrides, for such comparisons)
+  static const int nh_env = [] {
+    const char* e = getenv("QVGGT_ROPE_NH");
+    return e ? atoi(e) : 0;
+  }();
+  int nh = nh_env == 1 || nh_env == 2 || nh_env == 4 ? nh_env : 2;
+  while (H % nh) nh >>= 1;
+  const long total = T * 2 * (H / nh) * 4;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
-  hipLaunchKernelGGL(rope2d_kernel, grid, block, 0, (hipStream_t)stream, (const uint16_t*)qkv, (uint16_t*)out,
-                     positions, cos_table, sin_table, (int)table_rows, (int)T, (int)H, (long)src_token_stride,
-                     (long)dst_token_stride, (long)dst_part_stride);
+#define QV_ROPE2D(NH)                                                                                          \
+  hipLaunchKernelGGL(rope2d_kernel<NH>, grid, block, 0, (hipStream_t)stream, (const uint16_t*)qkv,           \
+                     (uint16_t*)out, positions, cos_table, sin_table, (int)table_rows, (int)T, (int)H,         \
+                     (long)src_token_stride, (long)dst_token_stride, (long)dst_part_stride)
+  if (nh == 4) QV_ROPE2D(4);
+  else if (nh == 2) QV_ROPE2D(2);
+  else QV_ROPE2D(1);
+#undef QV_ROPE2D
   return check_launch("rope2d");
 }
