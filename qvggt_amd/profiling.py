@@ -5,7 +5,7 @@
     python qvggt_amd/profiling.py aggregator [--frames S] [--w8a8]
     python qvggt_amd/profiling.py attention [--frames S] [--global] [--reps R]
     python qvggt_amd/profiling.py camera [--frames S] [--reps R] [--graph]
-    python qvggt_amd/profiling.py dense M K N [--bias]
+    python qvggt_amd/profiling.py dense M K N [--bias | --int8]
     python qvggt_amd/profiling.py sdpa [--frames S] [--global]
 
 ``copy`` launches one elementwise kernel that reads 512 MiB and writes
@@ -14,7 +14,14 @@ calibrate those counters against known byte counts.  ``gemm`` runs the W4A16
 linear (optionally with the fused bias + GELU epilogue) on seeded synthetic
 data; ``aggregator`` runs the VGGT aggregator forward twice (the first call
 warms up); ``attention`` runs frame (S sequences of 1374 tokens) or global
-(one sequence of S x 1374 tokens) attention over 16 heads on seeded data.  Every mode prints one line when done.
+(one sequence of S x 1374 tokens) attention over 16 heads on seeded data;
+``camera`` runs the W4-trunk camera head (4 iterations) on S seeded pose
+tokens, eager or replayed from a HIP graph, and prints the mean wall time per
+forward.  ``dense`` and ``sdpa`` time the vendor-library counterparts on the
+same shapes, for scale: an unquantised fp16 ``torch.mm`` / ``torch.addmm``
+(hipBLASLt), an int8 x int8 -> int32 ``torch._int_mm`` (hipBLASLt, the W8A8
+counterpart) and torch's ``scaled_dot_product_attention``, each replayed
+from a HIP graph after a 1 s warm-up.  Every mode prints one line when done.
 """
 from __future__ import annotations
 
@@ -134,10 +141,17 @@ def _replay_us(fn, reps=20, rounds=5):
     return e0.elapsed_time(e1) * 1e3 / (reps * rounds)
 
 
-def _dense(M, K, N, bias):
+def _dense(M, K, N, bias, int8=False):
     import torch
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(0)
+    if int8:
+        xi = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+        wi = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+        us = _replay_us(lambda: torch._int_mm(xi, wi.t()))
+        print(f"dense int8 _int_mm (int32 out): M={M} K={K} N={N}, {us:.1f} us, "
+              f"{2 * M * N * K / us / 1e6:.1f} TOPS", flush=True)
+        return
     x = torch.randn(M, K, generator=g).half().to(dev)
     w = torch.randn(N, K, generator=g).half().to(dev)
     b = torch.randn(N, generator=g).half().to(dev)
@@ -186,6 +200,7 @@ def main(argv=None):
     d.add_argument("K", type=int)
     d.add_argument("N", type=int)
     d.add_argument("--bias", action="store_true")
+    d.add_argument("--int8", action="store_true")
     q = sub.add_parser("sdpa")
     q.add_argument("--frames", type=int, default=8)
     q.add_argument("--global", dest="glob", action="store_true")
@@ -199,7 +214,7 @@ def main(argv=None):
     elif args.mode == "camera":
         _camera(args.frames, args.reps, args.graph)
     elif args.mode == "dense":
-        _dense(args.M, args.K, args.N, args.bias)
+        _dense(args.M, args.K, args.N, args.bias, args.int8)
     elif args.mode == "sdpa":
         _sdpa(args.frames, args.glob)
     else:
