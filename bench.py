@@ -177,6 +177,29 @@ def kernel_suite(dev):
 
     r = {}
     f16 = dict(dtype=torch.float16, device=dev)
+    # config 1: one W4A16 qkv linear on one frame (M = 1374, 1024 -> 3072, + bias)
+    xq, qwq, sq, zq = synthetic_w4(1374, 1024, 3072, seed=3, dev=dev)
+    bq_ = torch.zeros(3072, **f16)
+    oq = torch.empty(1374, 3072, **f16)
+    us = _time_graph(lambda i: E.w4a16_linear(xq, qwq, sq, zq, bias=bq_, epilogue=1, out=oq), 50)
+    r["w4a16_qkv_M1374"] = {"us": round(us, 2), "TFLOP/s": round(2.0 * 1374 * 3072 * 1024 / us / 1e6, 1)}
+    del xq, qwq, sq, zq, oq
+    # configs 3 and 4: one W4A16 frame block at S = 8 and one global block at
+    # S = 32 (LN, qkv, qk-norm + 2-D RoPE, attention, proj, LN, fc1 + GELU, fc2)
+    from qvggt_amd import aggregator as AG
+    agg1 = AG.Aggregator.random(w8a8=False, seed=4, device=dev, depth=1)
+    tables = E.rope2d_tables(AG.GRID + 1, 100.0, device=dev)
+    for name, S, blk, glob in (("frame_block_S8", 8, agg1.frame_blocks[0], False),
+                               ("global_block_S32", 32, agg1.global_blocks[0], True)):
+        Mb = S * AG.TOKENS
+        xb = torch.randn(Mb, AG.DIM, **f16)
+        ws = agg1._workspace(Mb, dev)
+        posb = AG.vggt_positions(S, dev)
+        us = _time_graph(lambda i: blk(xb, Mb if glob else AG.TOKENS, posb, tables, ws), 2 if glob else 10)
+        r[name] = {"us": round(us, 1), "tokens": Mb}
+        del xb
+    del agg1
+    agg1 = None
     M, D = 32 * 1374, 1024                                     # S = 32 tokens
     nb = 6                                                     # 6 x 180 MB rotating sets
     xs = [torch.randn(M, D, **f16) for _ in range(nb)]

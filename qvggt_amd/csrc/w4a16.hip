@@ -494,12 +494,11 @@ static int launch_gemm_cfg(const void* x, const void* qw, const void* s, const v
   return check_launch("w4a16_gemm");
 }
 
-// Tile choice.  Candidates: streamed kernel with BM = 128 / 96 / 64 (x 256)
-// and the 128 x 128 register-staged kernel; two workgroups run per CU (512
-// slots on 256 CUs).  Score = useful fraction of the occupied slot-rounds
-// times a per-tile efficiency prior (larger BM amortises the dequantisation
-// over more MFMAs).  M <= 64 goes to the skinny kernel, whose grid covers the
-// channels instead of M x N tiles.  QVGGT_W4_TILE=s128|s96|s64|n128|skinny
+// Tile choice (w4_pick_tile): streamed kernel with BM = 128 / 96 / 64 / 32
+// (x 256); two workgroups run per CU (512 slots on 256 CUs).  M <= 64 goes to
+// the skinny kernel, whose grid covers the channels instead of M x N tiles.
+// The 128 x 128 register-staged kernel measured slower at every VGGT shape
+// and is kept for comparison runs.  QVGGT_W4_TILE=s128|s96|s64|s32|n128|skinny
 // forces one (tuning).
 static int w4_tile_override() {
   static int v = [] {
@@ -510,6 +509,7 @@ static int w4_tile_override() {
     if (!strcmp(e, "s64")) return 3;
     if (!strcmp(e, "n128")) return 4;
     if (!strcmp(e, "skinny")) return 5;
+    if (!strcmp(e, "s32")) return 6;
     return 0;
   }();
   return v;
@@ -533,16 +533,22 @@ static int w4_pick_tile(int M, int N, int K) {
   const int ov = w4_tile_override();
   if (ov) return (ov == 5 && !skinny_ok) ? 1 : ov;
   if (skinny_ok) return 5;
-  const struct { int id, bm, bn; double prior; } cand[] = {
-      {1, 128, 256, 1.00}, {2, 96, 256, 0.93}, {3, 64, 256, 0.82}, {4, 128, 128, 0.70}};
-  const double slots = 512.0;
-  int best = 4;
-  double best_score = -1.0;
+  // Estimated time per candidate, in units of one 32-row tile step:
+  //  * at most one tile per CU (256 tiles): latency-bound, a tile costs its
+  //    pipeline fill + epilogue (~130 rows' worth) plus its rows;
+  //  * more: ceil(tiles / 512 slots) rounds of (130 + bm) / eff, eff the
+  //    measured per-row efficiency of the tile (larger tiles spread the
+  //    dequantisation over more MFMAs).
+  // Fitted to single-launch timings at M = 1374 .. 43968, K = 1024 / 4096,
+  // N = 1024 .. 4096 (the W4 linears of the VGGT blocks); it picks the
+  // measured fastest tile at each of them.
+  const struct { int id, bm; double eff; } cand[] = {{1, 128, 1.00}, {2, 96, 0.93}, {3, 64, 0.82}, {6, 32, 0.62}};
+  int best = 1;
+  double best_t = 1e300;
   for (const auto& c : cand) {
-    const double tiles = (double)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-    const double rounds = __builtin_ceil(tiles / slots);
-    const double score = ((double)M * N) / (rounds * slots * c.bm * c.bn) * c.prior;
-    if (score > best_score) { best_score = score; best = c.id; }
+    const double tiles = (double)((M + c.bm - 1) / c.bm) * ((N + 255) / 256);
+    const double t = tiles <= 256.0 ? 130.0 + c.bm : __builtin_ceil(tiles / 512.0) * (130.0 + c.bm) / c.eff;
+    if (t < best_t) { best_t = t; best = c.id; }
   }
   return best;
 }
@@ -559,6 +565,7 @@ static int launch_gemm(const void* x, const void* qw, const void* s, const void*
     case 2: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 96, st);
     case 3: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 64, st);
     case 5: return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st);
+    case 6: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 32, st);
     default: return launch_gemm_cfg<BF16, 128, 128, 64, 64>(x, qw, s, z, bias, out, M, N, K, epi, st);
   }
 }

@@ -144,7 +144,7 @@ __device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, cons
   epilogue_store4<BF16, EPI>(out, bias, v[0], v[1], v[2], v[3], m, n, N);
 }
 
-// Streamed (LDS-pipelined, 32x32 MFMA) GEMM, tile bm x 256 with bm in {64, 96, 128}.
+// Streamed (LDS-pipelined, 32x32 MFMA) GEMM, tile bm x 256 with bm in {32, 64, 96, 128}.
 template <bool BF16>
 int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                         void* out, int M, int N, int K, int epi, int bm, hipStream_t st);

@@ -234,7 +234,8 @@ int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void
                         void* out, int M, int N, int K, int epi, int bm, hipStream_t st) {
   if (bm == 128) launch_mt<BF16, 4>(x, qw, s, z, bias, out, M, N, K, epi, st);
   else if (bm == 96) launch_mt<BF16, 3>(x, qw, s, z, bias, out, M, N, K, epi, st);
-  else launch_mt<BF16, 2>(x, qw, s, z, bias, out, M, N, K, epi, st);
+  else if (bm == 64) launch_mt<BF16, 2>(x, qw, s, z, bias, out, M, N, K, epi, st);
+  else launch_mt<BF16, 1>(x, qw, s, z, bias, out, M, N, K, epi, st);
   return check_launch("w4a16_stream32");
 }
 
