@@ -60,7 +60,9 @@ int qv_w4a16_gemm(const void* x, const void* qweight, const void* scales,
                   void* stream);
 
 /*
- * Skinny-M W4A16 GEMV, 1 <= M <= 16 (wavefront reductions, no MFMA).
+ * Skinny-M W4A16 GEMV, 1 <= M <= 16 (channels across the grid, 128-k groups
+ * across the waves of a workgroup, products on 16x16x32 MFMA, wave partials
+ * summed through LDS; the GEMM entry runs M <= 64 on the same kernel).
  * Replaces gemv_forward_cuda_new (quantization_new/gemv/gemv_cuda.h:4-12,
  * gemv_cuda.cu:197-281; the reference accepts M in 1..7 and group 128 only).
  */
@@ -78,6 +80,22 @@ int qv_w4a16_gemv(const void* x, const void* qweight, const void* scales,
 int qv_w4a16_dequant(const void* qweight, const void* scales,
                      const void* scaled_zeros, void* out_w, int64_t N,
                      int64_t K, int dtype, void* stream);
+
+/*
+ * W4A16 linear fused with the LayerScale residual update of a VGGT block:
+ * residual[M,N] = residual + gamma[n] * fp16_rn(x . dequant(W)^T + bias[n]),
+ * the linear output rounded to the 16-bit type first and the update in fp32
+ * with one rounding (the order of `x.addcmul_(proj(h), gamma)` in torch).
+ * Same operands and layout checks as qv_w4a16_gemm; bias and gamma (N) are
+ * required, residual is read and written in place (16-byte aligned).  The
+ * reference has no counterpart: the update is vggt-hf's `x + ls(attn(...))` /
+ * `x + ls(mlp(...))` around the quantised proj / fc2 linears
+ * (qmodule.py:331-369 computes the linear, then torch adds).
+ */
+int qv_w4a16_gemm_residual(const void* x, const void* qweight, const void* scales,
+                           const void* scaled_zeros, const void* bias, const void* gamma,
+                           void* residual, int64_t M, int64_t N, int64_t K, int dtype,
+                           void* stream);
 
 /*
  * Quantise + pack: the buffers WQLinear.from_linear stores

@@ -118,6 +118,17 @@ def quantize_w4(linear: nn.Linear, group: int = 128) -> WQLinear:
     return WQLinear.from_linear(linear, 4, group, scales=s.half(), zeros=z.half())
 
 
+def _linear_residual(layer, x: torch.Tensor, gamma: torch.Tensor, resid: torch.Tensor, out: torch.Tensor):
+    """resid += gamma * layer(x): a block's proj / fc2 with its LayerScale
+    residual update, fused into the W4A16 epilogue when the layer is a
+    ``WQLinear`` with a bias; otherwise the linear, then torch's addcmul."""
+    if isinstance(layer, WQLinear) and layer.bias is not None:
+        E.w4a16_linear_residual(x, layer.qweight, layer.scales, layer.scaled_zeros, layer.bias, gamma, resid)
+        return resid
+    o = _linear(layer, x, QV_EPI_BIAS if layer.bias is not None else 0, out)
+    return resid.addcmul_(o, gamma)
+
+
 def _linear(layer, x: torch.Tensor, epilogue: int, out: torch.Tensor) -> torch.Tensor:
     """One linear of an AA block: ``WQLinear`` on the W4A16 kernels with the
     bias (+ GELU) fused, or an unquantised fp16 ``nn.Linear`` (blocks a
@@ -186,22 +197,22 @@ class AABlock(nn.Module):
         att = E.attention(v3[:, 0], v3[:, 1], v3[:, 2], seq_len, out=ws["att"].view(M, HEADS, HEAD_DIM))
         att = att.view(M, DIM)
         if not self.w8a8:
-            o = _linear(a.proj, att, QV_EPI_BIAS, ws["o"])
+            _linear_residual(a.proj, att, self.ls1.gamma, x, ws["o"])
         else:
             E.invoke_quant(ws["q8"], att, ws["s8"])
             o = a.proj(ws["q8"], ws["s8"], out=ws["o"])
-        x.addcmul_(o, self.ls1.gamma)
+            x.addcmul_(o, self.ls1.gamma)
         m = self.mlp
         if not self.w8a8:
             h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, BLOCK_LN_EPS, out=ws["h"])
             f = _linear(m.fc1, h, QV_EPI_BIAS_GELU, ws["f"])
-            o = _linear(m.fc2, f, QV_EPI_BIAS, ws["o"])
+            _linear_residual(m.fc2, f, self.ls2.gamma, x, ws["o"])
         else:
             E.rms_norm_general(ws["q8"], x, self.norm2.weight, self.norm2.bias, ws["s8"], BLOCK_LN_EPS, True)
             f = m.fc1(ws["q8"], ws["s8"], out=ws["f"])
             E.gelu_and_quant(ws["q8f"], f, ws["s8"], ws["ftmp"])
             o = m.fc2(ws["q8f"], ws["s8"], out=ws["o"])
-        x.addcmul_(o, self.ls2.gamma)
+            x.addcmul_(o, self.ls2.gamma)
         return x
 
 

@@ -133,6 +133,32 @@ def w4a16_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+def w4a16_linear_residual(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
+                          scaled_zeros: torch.Tensor, bias: torch.Tensor, gamma: torch.Tensor,
+                          residual: torch.Tensor) -> torch.Tensor:
+    """residual += gamma * fp16(x @ dequant(W)^T + bias), in place: a VGGT block's
+    proj / fc2 linear fused with its LayerScale residual update
+    (``x.addcmul_(linear(h), gamma)``).  Returns ``residual``."""
+    what = "w4a16_linear_residual"
+    dev = _on_gpu(x, qweight, scales, scaled_zeros, bias, gamma, residual, what=what)
+    dt = _dtype_code(x, what)
+    x = _contig(x)
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    N = qweight.shape[0] * 4
+    _check_w4_tables(qweight, scales, scaled_zeros, N, K, x.dtype, what)
+    for name, t in (("bias", bias), ("gamma", gamma)):
+        if t.dtype != x.dtype or t.numel() != N:
+            _fail(f"{what}: {name} must be ({N},) {x.dtype}")
+    if residual.dtype != x.dtype or residual.numel() != M * N or not residual.is_contiguous():
+        _fail(f"{what}: residual must be a contiguous {x.dtype} tensor of {M} x {N} elements")
+    with _device(dev):
+        _lib.call("qv_w4a16_gemm_residual", _ptr(x), _ptr(_contig(qweight)), _ptr(_contig(scales)),
+                  _ptr(_contig(scaled_zeros)), _ptr(_contig(bias)), _ptr(_contig(gamma)), _ptr(residual),
+                  M, N, K, dt, _stream(dev))
+    return residual
+
+
 def gemm_forward_cuda_new(in_feats: torch.Tensor, kernel: torch.Tensor, scales: torch.Tensor,
                           zeros: torch.Tensor) -> torch.Tensor:
     """out[..., N] = in_feats[..., K] @ dequant(kernel)^T; N = kernel.size(0) * 4.

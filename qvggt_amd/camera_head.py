@@ -35,7 +35,7 @@ import torch.nn.functional as F
 
 from . import awq_inference_engine as E
 from ._lib import QV_EPI_BIAS, QV_EPI_BIAS_GELU
-from .aggregator import LayerScale, Mlp, _linear, quantize_w4
+from .aggregator import LayerScale, Mlp, _linear, _linear_residual, quantize_w4
 
 DIM = 2048
 HEADS = 16
@@ -70,12 +70,10 @@ class TrunkBlock(nn.Module):
         q, k, v = qkv.float().view(S, 3, HEADS, HEAD_DIM).permute(1, 2, 0, 3)   # (H, S, 128) each
         a = torch.softmax(torch.bmm(q, k.transpose(1, 2).contiguous()) * HEAD_DIM ** -0.5, dim=-1) @ v
         att = a.permute(1, 0, 2).reshape(S, DIM).half()
-        o = _linear(self.attn.proj, att, QV_EPI_BIAS, torch.empty(S, DIM, dtype=x.dtype, device=x.device))
-        x.addcmul_(o, self.ls1.gamma)
+        _linear_residual(self.attn.proj, att, self.ls1.gamma, x, torch.empty(S, DIM, dtype=x.dtype, device=x.device))
         h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, LN_EPS)
         f = _linear(self.mlp.fc1, h, QV_EPI_BIAS_GELU, torch.empty(S, MLP_DIM, dtype=x.dtype, device=x.device))
-        o = _linear(self.mlp.fc2, f, QV_EPI_BIAS, torch.empty(S, DIM, dtype=x.dtype, device=x.device))
-        x.addcmul_(o, self.ls2.gamma)
+        _linear_residual(self.mlp.fc2, f, self.ls2.gamma, x, torch.empty(S, DIM, dtype=x.dtype, device=x.device))
         return x
 
 

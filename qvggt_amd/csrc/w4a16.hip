@@ -245,7 +245,8 @@ template <bool BF16, int MB, int NB>
 __global__ __launch_bounds__(1024) void w4a16_skinny_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K, int epi) {
+    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out,
+    int M, int N, int K, int epi) {
   __shared__ f32x4 red[16][MB][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -362,8 +363,11 @@ __global__ __launch_bounds__(1024) void w4a16_skinny_kernel(
       float v = 0.f;
       for (int w = 0; w < nwaves; ++w) v += red[w][mb][l][r];
       const int nn = n0 + 16 * j + 4 * (l >> 4) + r;
-      if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU) v += to_f32(bias[nn], BF16);
+      if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU || epi == QV_EPI_BIAS_RESID) v += to_f32(bias[nn], BF16);
       if (epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU) v = gelu_erf(v);
+      if (epi == QV_EPI_BIAS_RESID)  // out + gamma * o, o rounded first (resid_update8)
+        v = to_f32(out[(size_t)m * N + nn], BF16) +
+            to_f32(from_f32<BF16>(v), BF16) * to_f32(gamma[nn], BF16);
       out[(size_t)m * N + nn] = from_f32<BF16>(v);
     }
   }
@@ -555,17 +559,20 @@ static int w4_pick_tile(int M, int N, int K) {
 
 template <bool BF16>
 static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                         void* out, int M, int N, int K, int epi, hipStream_t st);
+                         void* out, int M, int N, int K, int epi, hipStream_t st,
+                         const void* gamma = nullptr);
 
 template <bool BF16>
 static int launch_gemm(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                       void* out, int M, int N, int K, int epi, hipStream_t st) {
-  switch (w4_pick_tile(M, N, K)) {
-    case 1: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 128, st);
-    case 2: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 96, st);
-    case 3: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 64, st);
-    case 5: return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st);
-    case 6: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, out, M, N, K, epi, 32, st);
+                       void* out, int M, int N, int K, int epi, hipStream_t st, const void* gamma = nullptr) {
+  int tile = w4_pick_tile(M, N, K);
+  if (tile == 4 && epi == QV_EPI_BIAS_RESID) tile = 1;  // the 128 x 128 kernel has no residual epilogue
+  switch (tile) {
+    case 1: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 128, st);
+    case 2: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 96, st);
+    case 3: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 64, st);
+    case 5: return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st, gamma);
+    case 6: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 32, st);
     default: return launch_gemm_cfg<BF16, 128, 128, 64, 64>(x, qw, s, z, bias, out, M, N, K, epi, st);
   }
 }
@@ -604,7 +611,7 @@ static int w4_skinny_nb(int M, int N) {
 
 template <bool BF16>
 static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                         void* out, int M, int N, int K, int epi, hipStream_t st) {
+                         void* out, int M, int N, int K, int epi, hipStream_t st, const void* gamma) {
   const int KT = K / 128;
   const int waves = KT < 16 ? KT : 16;
   const int nb = w4_skinny_nb(M, N);
@@ -612,7 +619,7 @@ static int launch_skinny(const void* x, const void* qw, const void* s, const voi
 #define QV_SKINNY(MB, NB)                                                                         \
   hipLaunchKernelGGL((w4a16_skinny_kernel<BF16, MB, NB>), grid, block, 0, st, (const uint16_t*)x, \
                      (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,                 \
-                     (const uint16_t*)bias, (uint16_t*)out, M, N, K, epi)
+                     (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, epi)
 #define QV_SKINNY_M(NB)            \
   if (M <= 16) QV_SKINNY(1, NB);   \
   else if (M <= 32) QV_SKINNY(2, NB); \
@@ -738,4 +745,20 @@ extern "C" int qv_w4a16_pack(const void* weight, const void* scales, const void*
                        (const uint16_t*)zeros, (uint16_t*)scales_out, (uint16_t*)scaled_zeros_out, (int)N, G, (int)rows);
   }
   return check_launch("w4a16_pack");
+}
+
+extern "C" int qv_w4a16_gemm_residual(const void* x, const void* qweight, const void* scales,
+                                      const void* scaled_zeros, const void* bias, const void* gamma,
+                                      void* residual, int64_t M, int64_t N, int64_t K, int dtype, void* stream) {
+  int rc = check_common(x, qweight, scales, scaled_zeros, bias, residual, M, N, K, dtype, QV_EPI_BIAS);
+  if (rc) return rc;
+  QV_CHECK_ARG(gamma != nullptr && ((uintptr_t)gamma % 16) == 0, "gamma must be a 16-byte aligned pointer");
+  QV_CHECK_ARG(((uintptr_t)residual % 16) == 0, "residual must be 16-byte aligned");
+  if (M == 0) return QV_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == QV_BF16)
+    return launch_gemm<true>(x, qweight, scales, scaled_zeros, bias, residual, (int)M, (int)N, (int)K,
+                             QV_EPI_BIAS_RESID, st, gamma);
+  return launch_gemm<false>(x, qweight, scales, scaled_zeros, bias, residual, (int)M, (int)N, (int)K,
+                            QV_EPI_BIAS_RESID, st, gamma);
 }

@@ -98,11 +98,16 @@ __device__ __forceinline__ size_t qw_chunk_u32(int n, int kt, int g, int K) {
          (g & 1) * 4;
 }
 
+// Internal epilogue id (not part of the qv_w4a16_gemm contract): bias, then
+// the LayerScale residual update out = out + gamma * fp16(acc + bias), in
+// place on the residual stream (qv_w4a16_gemm_residual).
+constexpr int QV_EPI_BIAS_RESID = 4;
+
 // Bias / GELU on four consecutive channels n..n+3 (fp32, before the single
 // rounding to the 16-bit output type).
 template <bool BF16, int EPI>
 __device__ __forceinline__ void epilogue_apply4(const uint16_t* __restrict__ bias, float (&r)[4], int n) {
-  if constexpr (EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU) {
+  if constexpr (EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_BIAS_RESID) {
     const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
     r[0] += to_f32((uint16_t)(b.x & 0xFFFF), BF16);
     r[1] += to_f32((uint16_t)(b.x >> 16), BF16);
@@ -113,6 +118,24 @@ __device__ __forceinline__ void epilogue_apply4(const uint16_t* __restrict__ bia
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = gelu_erf(r[i]);
   }
+}
+
+// Residual update of 8 consecutive channels: r + o * g per element in fp32,
+// o the already rounded 16-bit linear output, one rounding of the result (the
+// order of torch's x.addcmul_(o, gamma) on 16-bit tensors).
+template <bool BF16>
+__device__ __forceinline__ uint4 resid_update8(const uint4& r, const uint4& o, const uint4& g) {
+  const uint32_t rw[4] = {r.x, r.y, r.z, r.w}, ow[4] = {o.x, o.y, o.z, o.w}, gw[4] = {g.x, g.y, g.z, g.w};
+  uint32_t res[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = to_f32((uint16_t)(rw[i] & 0xFFFF), BF16) +
+                     to_f32((uint16_t)(ow[i] & 0xFFFF), BF16) * to_f32((uint16_t)(gw[i] & 0xFFFF), BF16);
+    const float hi = to_f32((uint16_t)(rw[i] >> 16), BF16) +
+                     to_f32((uint16_t)(ow[i] >> 16), BF16) * to_f32((uint16_t)(gw[i] >> 16), BF16);
+    res[i] = pack2<BF16>(lo, hi);
+  }
+  return make_uint4(res[0], res[1], res[2], res[3]);
 }
 
 // Bias / GELU epilogue on four consecutive channels n..n+3 of token m, one
@@ -147,6 +170,6 @@ __device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, cons
 // Streamed (LDS-pipelined, 32x32 MFMA) GEMM, tile bm x 256 with bm in {32, 64, 96, 128}.
 template <bool BF16>
 int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                        void* out, int M, int N, int K, int epi, int bm, hipStream_t st);
+                        const void* gamma, void* out, int M, int N, int K, int epi, int bm, hipStream_t st);
 
 }  // namespace qv

@@ -30,7 +30,8 @@ template <bool BF16, int MT, int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
                            const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-                           const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N,
+                           const uint16_t* __restrict__ bias, const uint16_t* __restrict__ gamma,
+                           uint16_t* __restrict__ out, int M, int N,
                            int K, int tiles_n) {
   constexpr int BM = 32 * MT, BN = 256, NT = 2;
   constexpr int A_BYTES = BM * 128, B_BYTES = BN * 32, S_BYTES = BN * 2;
@@ -199,19 +200,24 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
     const int idx = it * 64 + lane;
     const int row = idx >> 3, c = idx & 7;
     const int m = m0 + row, n = n0 + 64 * wave + 8 * c;
-    if (m < M && n < N)
-      *reinterpret_cast<uint4*>(out + (size_t)m * N + n) = *reinterpret_cast<const uint4*>(stg + row * EP + c * 16);
+    if (m < M && n < N) {
+      uint4 v = *reinterpret_cast<const uint4*>(stg + row * EP + c * 16);
+      if constexpr (EPI == QV_EPI_BIAS_RESID)
+        v = resid_update8<BF16>(*reinterpret_cast<const uint4*>(out + (size_t)m * N + n), v,
+                                *reinterpret_cast<const uint4*>(gamma + n));
+      *reinterpret_cast<uint4*>(out + (size_t)m * N + n) = v;
+    }
   }
 }
 
 template <bool BF16, int MT>
 static void launch_mt(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                      void* out, int M, int N, int K, int epi, hipStream_t st) {
+                      const void* gamma, void* out, int M, int N, int K, int epi, hipStream_t st) {
   const int tiles_m = (M + 32 * MT - 1) / (32 * MT), tiles_n = (N + 255) / 256;
   const dim3 grid(tiles_m * tiles_n), block(256);
 #define QV_ARGS                                                                                \
   (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,             \
-      (const uint16_t*)bias, (uint16_t*)out, M, N, K, tiles_n
+      (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, tiles_n
   switch (epi) {
     case QV_EPI_NONE:
       hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_NONE>), grid, block, 0, st, QV_ARGS);
@@ -222,8 +228,11 @@ static void launch_mt(const void* x, const void* qw, const void* s, const void* 
     case QV_EPI_BIAS_GELU:
       hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_BIAS_GELU>), grid, block, 0, st, QV_ARGS);
       break;
-    default:
+    case QV_EPI_GELU:
       hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_GELU>), grid, block, 0, st, QV_ARGS);
+      break;
+    default:
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_BIAS_RESID>), grid, block, 0, st, QV_ARGS);
       break;
   }
 #undef QV_ARGS
@@ -231,17 +240,17 @@ static void launch_mt(const void* x, const void* qw, const void* s, const void* 
 
 template <bool BF16>
 int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                        void* out, int M, int N, int K, int epi, int bm, hipStream_t st) {
-  if (bm == 128) launch_mt<BF16, 4>(x, qw, s, z, bias, out, M, N, K, epi, st);
-  else if (bm == 96) launch_mt<BF16, 3>(x, qw, s, z, bias, out, M, N, K, epi, st);
-  else if (bm == 64) launch_mt<BF16, 2>(x, qw, s, z, bias, out, M, N, K, epi, st);
-  else launch_mt<BF16, 1>(x, qw, s, z, bias, out, M, N, K, epi, st);
+                        const void* gamma, void* out, int M, int N, int K, int epi, int bm, hipStream_t st) {
+  if (bm == 128) launch_mt<BF16, 4>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st);
+  else if (bm == 96) launch_mt<BF16, 3>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st);
+  else if (bm == 64) launch_mt<BF16, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st);
+  else launch_mt<BF16, 1>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st);
   return check_launch("w4a16_stream32");
 }
 
 template int launch_w4a16_stream<false>(const void*, const void*, const void*, const void*, const void*,
-                                        void*, int, int, int, int, int, hipStream_t);
+                                        const void*, void*, int, int, int, int, int, hipStream_t);
 template int launch_w4a16_stream<true>(const void*, const void*, const void*, const void*, const void*,
-                                       void*, int, int, int, int, int, hipStream_t);
+                                       const void*, void*, int, int, int, int, int, hipStream_t);
 
 }  // namespace qv

@@ -216,3 +216,29 @@ def test_wqlinear_forward(gpu):
     for xin in (x, x[:3]):   # GEMM path and GEMV path (M < 8)
         y = q(xin)
         assert O.rel_err(y.float().cpu().numpy(), ref[: xin.shape[0]]) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 4096), (40, 1024, 1024), (300, 1024, 4096), (1374, 1024, 1024),
+                                   (10992, 1024, 4096)])
+def test_linear_residual_matches_unfused(gpu, M, N, K):
+    """residual += gamma * fp16(x W^T + b) in the GEMM epilogue (skinny kernel at
+    M <= 64, stream tiles above) equals the linear followed by the fp32
+    update, to one fp16 ulp (fma contraction of the update may differ)."""
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd._lib import QV_EPI_BIAS
+    p = O.make_w4_problem(M, K, N, seed=M + 3)
+    t = _to_dev(p, gpu)
+    g = torch.Generator(device=gpu).manual_seed(M)
+    bias = (torch.randn(N, generator=g, device=gpu) * 0.1).half()
+    gamma = (torch.rand(N, generator=g, device=gpu) + 0.5).half()
+    resid = torch.randn(M, N, generator=g, device=gpu).half()
+    o = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=bias, epilogue=QV_EPI_BIAS)
+    want = (resid.float() + o.float() * gamma.float()).half()
+    got = resid.clone()
+    E.w4a16_linear_residual(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias, gamma, got)
+    torch.cuda.synchronize()
+    d = (got.float() - want.float()).abs()
+    ulp = torch.from_numpy(np.spacing(np.abs(want.cpu().numpy())).astype(np.float32)).to(gpu)
+    assert torch.isfinite(got.float()).all() and bool((d <= ulp).all()), d.max().item()
+    with pytest.raises(RuntimeError):
+        E.w4a16_linear_residual(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias, gamma[:16], got)
