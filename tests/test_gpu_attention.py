@@ -69,3 +69,51 @@ def test_attention_separate_buffers_and_determinism(gpu):
     assert torch.equal(o1, o2)
     ref = attention_ref(x[:, 0], x[:, 1], x[:, 2], B, L)
     assert np.abs(o1.float().cpu().numpy() - ref).max() / np.abs(ref).max() <= TOL
+
+
+@pytest.mark.parametrize("L", [63, 65, 127, 129, 257])
+def test_attention_tile_boundaries(gpu, L):
+    """Sequence lengths one below / above the 64-key tile and 256-query
+    workgroup sizes (masked last tile, idle query lanes)."""
+    from qvggt_amd import awq_inference_engine as E
+    x = _qkv(2 * L, 3, L)
+    xt = torch.from_numpy(x).to(gpu)
+    out = E.attention(xt[:, 0], xt[:, 1], xt[:, 2], L)
+    ref = attention_ref(x[:, 0], x[:, 1], x[:, 2], 2, L)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all() and np.abs(got - ref).max() / np.abs(ref).max() <= TOL
+
+
+def test_attention_rising_scores_force_rescales(gpu):
+    """Scores that grow by ~17 log2 units per 64-key tile: every tile's P
+    would exceed 2^8 against the previous reference, so the lazy rescale runs
+    on every tile; the last key dominates some queries outright."""
+    from qvggt_amd import awq_inference_engine as E
+    L, H = 640, 2
+    rng = np.random.default_rng(7)
+    x = (0.1 * rng.standard_normal((L, 3, H, 64))).astype(np.float32)
+    x[:, 0, :, 0] = 8.0                                     # q along dim 0
+    x[:, 1, :, 0] = np.linspace(-60.0, 60.0, L)[:, None]    # k rises along the sequence
+    x = x.astype(np.float16)
+    xt = torch.from_numpy(x).to(gpu)
+    out = E.attention(xt[:, 0], xt[:, 1], xt[:, 2], L)
+    ref = attention_ref(x[:, 0], x[:, 1], x[:, 2], 1, L)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all() and np.abs(got - ref).max() / np.abs(ref).max() <= TOL
+
+
+def test_attention_large_and_falling_scores(gpu):
+    """Large-magnitude scores (|s| * scale up to ~100): the first tile holds the
+    maxima and later tiles underflow to P = 0 in fp16 without NaNs."""
+    from qvggt_amd import awq_inference_engine as E
+    L, H = 512, 2
+    rng = np.random.default_rng(8)
+    x = (0.1 * rng.standard_normal((L, 3, H, 64))).astype(np.float32)
+    x[:, 0, :, :4] = 8.0
+    x[:, 1, :, :4] = np.linspace(25.0, -25.0, L)[:, None, None]
+    x = x.astype(np.float16)
+    xt = torch.from_numpy(x).to(gpu)
+    out = E.attention(xt[:, 0], xt[:, 1], xt[:, 2], L)
+    ref = attention_ref(x[:, 0], x[:, 1], x[:, 2], 1, L)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all() and np.abs(got - ref).max() / np.abs(ref).max() <= TOL
