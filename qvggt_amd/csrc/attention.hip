@@ -210,6 +210,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
               st == 0 ? f32x16{} - base[qb] : sc[qb][kb], 0, 0, 0);
       }
     }
+    // ---- V^T fragments of this tile, read before the softmax so their LDS
+    // latency hides behind it (the PV MFMAs below consume them)
+    const uint8_t* vb = v_lds[buf];
+    uint4 vfr[2][4];
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      const int dim = 32 * db + tr_dim;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        uint2 vv[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int key = 16 * st + 8 * r + tr_key;
+          vv[r] = lds_read_tr16(vb + key * 128 + (((dim >> 3) ^ fv(key)) * 16) + ((dim >> 2) & 1) * 8);
+        }
+        vfr[db][st] = make_uint4(vv[0].x, vv[0].y, vv[1].x, vv[1].y);
+      }
+    }
     uint4 pf[2][4];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
@@ -275,19 +293,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       l_run[qb] += t;
     }
     // ---- O^T += V^T P^T: each V^T fragment (16 contiguous bytes) feeds both query blocks
-    const uint8_t* vb = v_lds[buf];
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
-      const int dim = 32 * db + tr_dim;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        uint2 vv[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int key = 16 * st + 8 * r + tr_key;
-          vv[r] = lds_read_tr16(vb + key * 128 + (((dim >> 3) ^ fv(key)) * 16) + ((dim >> 2) & 1) * 8);
-        }
-        const uint4 vf = make_uint4(vv[0].x, vv[0].y, vv[1].x, vv[1].y);
+        const uint4 vf = vfr[db][st];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
           o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
