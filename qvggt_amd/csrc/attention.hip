@@ -6,7 +6,8 @@
 // token-major with arbitrary token strides and head stride 64, so q, k and v
 // can be read straight out of the fused qkv projection output.
 //
-// Workgroup: 4 waves, 64 queries each (256 queries of one (sequence, head)).
+// Workgroup: ATT_WAVES waves, 64 queries each (64 * ATT_WAVES queries of one
+// (sequence, head)).
 // Per 64-key tile a wave computes S^T = K Q^T for its two 32-query blocks
 // (2 x 2 x 4 v_mfma_f32_32x32x16_f16, every K fragment read from LDS feeding
 // both blocks), the online softmax in registers, and O^T += V^T P^T (16 more
@@ -36,7 +37,9 @@
 namespace qv {
 
 constexpr int ATT_QW = 64;                 // queries per wave (two 32-query blocks)
-constexpr int ATT_BQ = 4 * ATT_QW;         // queries per workgroup
+constexpr int ATT_WAVES = 4;               // waves per workgroup
+constexpr int ATT_BQ = ATT_WAVES * ATT_QW; // queries per workgroup
+constexpr int ATT_DMA = 8 / ATT_WAVES;     // 1 KB (8-key) DMA rows per wave per tile, K and V each
 constexpr int ATT_BK = 64;                 // keys per tile
 
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units: P <= 256 between rescales
@@ -81,7 +84,7 @@ __device__ __forceinline__ float half_sum(float x) {
   return a + b;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(
+__global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ out, int L, int H, long q_ts, long kv_ts, long v_ts, long o_ts, float scale_log2) {
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][ATT_BK * 128];
@@ -128,36 +131,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // ---- K tile DMA: 8 x 1 KB per tile, 2 per wave; lane L lands at key
   // r0 + L/8, physical chunk L%8, so it fetches logical chunk (L%8) ^ fk(row).
   const auto rsK = make_rsrc(k + tok0 * kv_ts + (long)head * 64, (uint64_t)L * kv_ts * 2);
-  uint32_t k_voff[2];
+  uint32_t k_voff[ATT_DMA];
 #pragma unroll
-  for (int w2 = 0; w2 < 2; ++w2) {
-    const int row = 8 * (2 * wave + w2) + (lane >> 3);
+  for (int w2 = 0; w2 < ATT_DMA; ++w2) {
+    const int row = 8 * (ATT_DMA * wave + w2) + (lane >> 3);
     const int c = (lane & 7) ^ fk(row);
     k_voff[w2] = (uint32_t)((lane >> 3) * kv_ts * 2 + c * 16);
   }
   const uint32_t klds0 = lds_addr(k_lds);
   auto issue_k = [&](int tile, int buf) {
 #pragma unroll
-    for (int w2 = 0; w2 < 2; ++w2) {
-      const int r0 = 8 * (2 * wave + w2);
+    for (int w2 = 0; w2 < ATT_DMA; ++w2) {
+      const int r0 = 8 * (ATT_DMA * wave + w2);
       lds_dma16(rsK, k_voff[w2], (uint32_t)((tile * ATT_BK + r0) * kv_ts * 2),
                 klds0 + buf * (ATT_BK * 128) + r0 * 128);
     }
   };
   // ---- V tile DMA, natural [key][dim] layout with the fv swizzle
   const auto rsV = make_rsrc(v + tok0 * v_ts + (long)head * 64, (uint64_t)L * v_ts * 2);
-  uint32_t v_voff[2];
+  uint32_t v_voff[ATT_DMA];
 #pragma unroll
-  for (int w2 = 0; w2 < 2; ++w2) {
-    const int row = 8 * (2 * wave + w2) + (lane >> 3);
+  for (int w2 = 0; w2 < ATT_DMA; ++w2) {
+    const int row = 8 * (ATT_DMA * wave + w2) + (lane >> 3);
     const int c = (lane & 7) ^ fv(row);
     v_voff[w2] = (uint32_t)((lane >> 3) * v_ts * 2 + c * 16);
   }
   const uint32_t vlds0 = lds_addr(v_lds);
   auto issue_v = [&](int tile, int buf) {
 #pragma unroll
-    for (int w2 = 0; w2 < 2; ++w2) {
-      const int r0 = 8 * (2 * wave + w2);
+    for (int w2 = 0; w2 < ATT_DMA; ++w2) {
+      const int r0 = 8 * (ATT_DMA * wave + w2);
       lds_dma16(rsV, v_voff[w2], (uint32_t)((tile * ATT_BK + r0) * v_ts * 2),
                 vlds0 + buf * (ATT_BK * 128) + r0 * 128);
     }
@@ -358,7 +361,7 @@ extern "C" int qv_attention_fwd(const void* q, const void* k, const void* v, voi
   const long nwg = B * H * qtiles;
   QV_CHECK_ARG(nwg <= INT32_MAX, "grid too large");
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(qv::attention_fwd_kernel, dim3((unsigned)nwg), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(qv::attention_fwd_kernel, dim3((unsigned)nwg), dim3(64 * qv::ATT_WAVES), 0, (hipStream_t)stream,
                      (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out, (int)L, (int)H,
                      (long)q_token_stride, (long)k_token_stride, (long)v_token_stride, (long)out_token_stride,
                      scale_log2);
