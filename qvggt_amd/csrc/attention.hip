@@ -102,6 +102,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
   const int head = (lid / qtiles) % H;
   const int seq = lid / (qtiles * H);
   const long tok0 = (long)seq * L;
+  const bool live = qt * ATT_BQ + wave * ATT_QW < L;   // wave-uniform
 
   // ---- Q^T fragments (B operand of S^T = K Q^T): per query block, 4 k-steps of 16 dims
   uint4 qf[2][4];
@@ -196,115 +197,119 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
       issue_k(j + 1, buf ^ 1);
       issue_v(j + 1, buf ^ 1);
     }
-    // ---- S^T = K Q^T for the 64 keys of tile j, both query blocks (raw dot products)
-    const uint8_t* kb_lds = k_lds[buf];
-    f32x16 sc[2][2];   // [query block][key block]
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int row = 32 * kb + l32;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int c = 2 * st + h;
-        const uint4 kf = *reinterpret_cast<const uint4*>(kb_lds + row * 128 + ((c ^ fk(row)) * 16));
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-          sc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-              __builtin_bit_cast(f16x8, kf), __builtin_bit_cast(f16x8, qf[qb][st]),
-              st == 0 ? f32x16{} - base[qb] : sc[qb][kb], 0, 0, 0);
-      }
-    }
-    // ---- V^T fragments of this tile, read before the softmax so their LDS
-    // latency hides behind it (the PV MFMAs below consume them)
-    const uint8_t* vb = v_lds[buf];
-    uint4 vfr[2][4];
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      const int dim = 32 * db + tr_dim;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        uint2 vv[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int key = 16 * st + 8 * r + tr_key;
-          vv[r] = lds_read_tr16(vb + key * 128 + (((dim >> 3) ^ fv(key)) * 16) + ((dim >> 2) & 1) * 8);
+    // a wave whose 64 queries all lie past the sequence end (the last query
+    // tile of a frame) only issues its share of the DMA and keeps the barriers
+    if (live) {
+      // ---- S^T = K Q^T for the 64 keys of tile j, both query blocks (raw dot products)
+      const uint8_t* kb_lds = k_lds[buf];
+      f32x16 sc[2][2];   // [query block][key block]
+  #pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int row = 32 * kb + l32;
+  #pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int c = 2 * st + h;
+          const uint4 kf = *reinterpret_cast<const uint4*>(kb_lds + row * 128 + ((c ^ fk(row)) * 16));
+  #pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            sc[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                __builtin_bit_cast(f16x8, kf), __builtin_bit_cast(f16x8, qf[qb][st]),
+                st == 0 ? f32x16{} - base[qb] : sc[qb][kb], 0, 0, 0);
         }
-        vfr[db][st] = make_uint4(vv[0].x, vv[0].y, vv[1].x, vv[1].y);
       }
-    }
-    uint4 pf[2][4];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      if (mask) {
-        const int key0 = j * ATT_BK + 4 * h;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (key0 + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[qb][kb][r] = -INFINITY;
-      }
-      // ---- P = 2^S' = 2^(S - m_use) in fp16 against the current reference,
-      // with this tile's partial row sum t (v_dot2 on the fp16 values).  The
-      // tile maximum is only needed when some P could exceed 2^RESCALE_SLACK,
-      // and every such P makes t exceed it too (P >= 0), so the maximum is
-      // computed only for waves where some lane's t does, and on the first
-      // tile (no reference yet).
-      float t = 0.f;
-      auto make_p = [&](bool shift, float off) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int pp = 0; pp < 2; ++pp) {
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float s0 = sc[qb][kb][8 * pp + 2 * e], s1 = sc[qb][kb][8 * pp + 2 * e + 1];
-              const float p0 = __builtin_amdgcn_exp2f(shift ? s0 + off : s0);
-              const float p1 = __builtin_amdgcn_exp2f(shift ? s1 + off : s1);
-              const f16x2 ph = {(_Float16)p0, (_Float16)p1};
-              t = __builtin_amdgcn_fdot2(ph, ones, t, false);
-              w[e] = __builtin_bit_cast(uint32_t, ph);
-            }
-            pf[qb][2 * kb + pp] = make_uint4(w[0], w[1], w[2], w[3]);
+      // ---- V^T fragments of this tile, read before the softmax so their LDS
+      // latency hides behind it (the PV MFMAs below consume them)
+      const uint8_t* vb = v_lds[buf];
+      uint4 vfr[2][4];
+  #pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const int dim = 32 * db + tr_dim;
+  #pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          uint2 vv[2];
+  #pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int key = 16 * st + 8 * r + tr_key;
+            vv[r] = lds_read_tr16(vb + key * 128 + (((dim >> 3) ^ fv(key)) * 16) + ((dim >> 2) & 1) * 8);
           }
-      };
-      make_p(false, 0.f);
-      if (__builtin_amdgcn_ballot_w64(!(t <= P_SUM_LIMIT) || m_use[qb] == -INFINITY)) {
-        // ---- tile maximum of this query (both lane halves hold 32 keys each)
-        float mx = sc[qb][0][0];
-#pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[qb][0][r]);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[qb][1][r]);
-        mx = half_max(mx) + base[qb];
-        // ---- lazy rescale: the reference moves when the tile maximum exceeds
-        // it by more than the slack; then P is recomputed against it
-        const bool need = mx > m_use[qb] + RESCALE_SLACK;
-        if (__builtin_amdgcn_ballot_w64(need)) {
-          const float m_new = need ? mx : m_use[qb];
-          const float alpha = __builtin_amdgcn_exp2f(m_use[qb] - m_new);  // 0 on the first tile, 1 if !need
-          m_use[qb] = m_new;
-          l_run[qb] *= alpha;
-#pragma unroll
-          for (int db = 0; db < 2; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
-          t = 0.f;
-          make_p(true, base[qb] - m_new);
+          vfr[db][st] = make_uint4(vv[0].x, vv[0].y, vv[1].x, vv[1].y);
         }
-        base[qb] = m_use[qb];
       }
-      l_run[qb] += t;
-    }
-    // ---- O^T += V^T P^T: each V^T fragment (16 contiguous bytes) feeds both query blocks
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const uint4 vf = vfr[db][st];
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-          o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
-                                                            __builtin_bit_cast(f16x8, pf[qb][st]), o[qb][db], 0, 0, 0);
+      uint4 pf[2][4];
+  #pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        if (mask) {
+          const int key0 = j * ATT_BK + 4 * h;
+  #pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (key0 + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[qb][kb][r] = -INFINITY;
+        }
+        // ---- P = 2^S' = 2^(S - m_use) in fp16 against the current reference,
+        // with this tile's partial row sum t (v_dot2 on the fp16 values).  The
+        // tile maximum is only needed when some P could exceed 2^RESCALE_SLACK,
+        // and every such P makes t exceed it too (P >= 0), so the maximum is
+        // computed only for waves where some lane's t does, and on the first
+        // tile (no reference yet).
+        float t = 0.f;
+        auto make_p = [&](bool shift, float off) {
+  #pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+              uint32_t w[4];
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float s0 = sc[qb][kb][8 * pp + 2 * e], s1 = sc[qb][kb][8 * pp + 2 * e + 1];
+                const float p0 = __builtin_amdgcn_exp2f(shift ? s0 + off : s0);
+                const float p1 = __builtin_amdgcn_exp2f(shift ? s1 + off : s1);
+                const f16x2 ph = {(_Float16)p0, (_Float16)p1};
+                t = __builtin_amdgcn_fdot2(ph, ones, t, false);
+                w[e] = __builtin_bit_cast(uint32_t, ph);
+              }
+              pf[qb][2 * kb + pp] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        };
+        make_p(false, 0.f);
+        if (__builtin_amdgcn_ballot_w64(!(t <= P_SUM_LIMIT) || m_use[qb] == -INFINITY)) {
+          // ---- tile maximum of this query (both lane halves hold 32 keys each)
+          float mx = sc[qb][0][0];
+  #pragma unroll
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[qb][0][r]);
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[qb][1][r]);
+          mx = half_max(mx) + base[qb];
+          // ---- lazy rescale: the reference moves when the tile maximum exceeds
+          // it by more than the slack; then P is recomputed against it
+          const bool need = mx > m_use[qb] + RESCALE_SLACK;
+          if (__builtin_amdgcn_ballot_w64(need)) {
+            const float m_new = need ? mx : m_use[qb];
+            const float alpha = __builtin_amdgcn_exp2f(m_use[qb] - m_new);  // 0 on the first tile, 1 if !need
+            m_use[qb] = m_new;
+            l_run[qb] *= alpha;
+  #pragma unroll
+            for (int db = 0; db < 2; ++db)
+  #pragma unroll
+              for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+            t = 0.f;
+            make_p(true, base[qb] - m_new);
+          }
+          base[qb] = m_use[qb];
+        }
+        l_run[qb] += t;
+      }
+      // ---- O^T += V^T P^T: each V^T fragment (16 contiguous bytes) feeds both query blocks
+  #pragma unroll
+      for (int db = 0; db < 2; ++db) {
+  #pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const uint4 vf = vfr[db][st];
+  #pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
+                                                              __builtin_bit_cast(f16x8, pf[qb][st]), o[qb][db], 0, 0, 0);
+        }
       }
     }
     if (more) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next K and V tiles landed
