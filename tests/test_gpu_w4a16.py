@@ -242,3 +242,27 @@ def test_linear_residual_matches_unfused(gpu, M, N, K):
     assert torch.isfinite(got.float()).all() and bool((d <= ulp).all()), d.max().item()
     with pytest.raises(RuntimeError):
         E.w4a16_linear_residual(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias, gamma[:16], got)
+
+
+@pytest.mark.parametrize("M", [4, 300])
+def test_noncontiguous_activations_match_contiguous(gpu, M):
+    """The ops read the activations through a contiguous copy when given a
+    strided view (the reference reads raw data_ptr whatever the strides): a
+    column slice of a wider tensor gives the same bits as its contiguous copy,
+    on the GEMV (M = 4) and GEMM (M = 300) entries."""
+    from qvggt_amd import awq_inference_engine as E
+    N, K = 1024, 1024
+    p = O.make_w4_problem(M, K, N, seed=11 + M)
+    t = _to_dev(p, gpu)
+    wide = torch.zeros(M, 2 * K, dtype=torch.float16, device=gpu)
+    wide[:, K // 2:K // 2 + K] = t["x"]
+    view = wide[:, K // 2:K // 2 + K]
+    assert not view.is_contiguous()
+    if M <= 7:
+        got = E.gemv_forward_cuda_new(view, t["qweight"], t["scales"], t["scaled_zeros"], M, N, K, 128)
+        want = E.gemv_forward_cuda_new(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], M, N, K, 128)
+    else:
+        got = E.gemm_forward_cuda_new(view, t["qweight"], t["scales"], t["scaled_zeros"])
+        want = E.gemm_forward_cuda_new(t["x"], t["qweight"], t["scales"], t["scaled_zeros"])
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
