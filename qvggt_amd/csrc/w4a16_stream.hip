@@ -2,26 +2,25 @@
 //
 // Workgroup tile BM (= 32*MT, m) x 256 (n); the 4 waves sit side by side
 // along n, each owning BM x 64 = MT x 2 tiles of v_mfma_f32_32x32x16 (so every
-// dequantised weight fragment feeds MT MFMAs of 32x32x16).  All operands
-// stream global -> LDS with direct buffer loads (no register staging) through
-// 3 stages of 64 k:
-//   A   BM rows x 128 B activations; 16-byte chunk c of row r stored at
-//       c ^ fA(r), fA(r) = (r & 7) ^ ((r >> 3) & 1)
-//   B   256 channels x 32 B: the stage's two 16-byte 32-k chunks per channel,
-//       chunk cc of channel n stored at cc ^ fB(n), fB(n) = ((n>>2) ^ (n>>3)) & 1
-//   S,Z the 256 fp16 scales / scaled zeros of the stage's 128-k group
-// Both swizzles make every 8-lane and every 16-lane group of a b128 read hit
-// distinct banks (whichever the hardware groups per cycle), and each 1 KB
-// direct write is contiguous.
+// dequantised weight fragment feeds MT MFMAs of 32x32x16).  The activations,
+// which all four waves read, stream global -> LDS with direct buffer loads
+// (no register staging) through 3 stages of 64 k: BM rows x 128 B, 16-byte
+// chunk c of row r stored at c ^ fA(r), fA(r) = (r & 7) ^ ((r >> 3) & 1), which
+// makes every 8-lane and every 16-lane group of a b128 read hit distinct banks
+// while each 1 KB direct write stays contiguous.  The packed weights and the
+// group scales / scaled zeros of a wave's own 64 channels go straight to its
+// registers with ordinary buffer loads one stage ahead: no other wave reads
+// them, and routing them through LDS cost more than its share (the direct
+// LDS writes of a stage contend with the fragment reads).
 //
 // K-slots: MFMA operand lanes split as h = lane/32 (k-half) and l = lane%32.
 // In k-step s (0..3) of a stage, lane half h takes 32-k chunk h and nibble
 // pair s of its four words, i.e. stage-local k = 32*h + 8*s + slot on BOTH
 // operands (activations: 8 contiguous halves of chunk 4h + s).  Output: lane
 // (h, l), register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the tile.
-// LDS per workgroup: 3 x (BM*128 + 9 KB); BM = 128 -> 75 KB, 2 workgroups/CU.
-// The epilogue reuses that LDS to stage each wave's BM x 64 output tile and
-// writes it back as whole 128-byte rows.
+// LDS per workgroup: max(3 stages x BM*128, the epilogue staging of 4 x BM x
+// 144 B); BM = 128 -> 72 KB, 2 workgroups/CU.  The epilogue stages each wave's
+// BM x 64 output tile there and writes it back as whole 128-byte rows.
 #include "w4a16_common.h"
 
 namespace qv {
@@ -34,13 +33,14 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
                            uint16_t* __restrict__ out, int M, int N,
                            int K, int tiles_n) {
   constexpr int BM = 32 * MT, BN = 256, NT = 2;
-  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 32, S_BYTES = BN * 2;
-  constexpr int STAGE = A_BYTES + B_BYTES + 2 * S_BYTES;
+  constexpr int A_BYTES = BM * 128;
+  constexpr int STAGE = A_BYTES;
   constexpr int NSTAGE = 3;
   constexpr int A_INSTR = BM / 32;                // 1 KB direct loads per wave for A
-  constexpr int VM_PER_STAGE = A_INSTR + 2 + 1;   // + B (2) + S or Z (1)
-  static_assert(VM_PER_STAGE < 16, "vmcnt immediate");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * STAGE];
+  static_assert(A_INSTR < 16, "vmcnt immediate");
+  constexpr int EP = 144;  // bytes per staged epilogue row: 64 fp16 + 16 B pad
+  constexpr int LDS_BYTES = NSTAGE * STAGE > 4 * BM * EP ? NSTAGE * STAGE : 4 * BM * EP;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -54,7 +54,8 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
 
   const auto rsA = make_rsrc(x + (size_t)m0 * K, (uint64_t)(M - m0) * K2);
   const auto rsB = make_rsrc(qw + (size_t)(n0 >> 2) * (K >> 1), (uint64_t)((N - n0) >> 2) * K2);
-  const auto rsS = make_rsrc((wave < 2 ? scales : zeros) + n0, ((uint64_t)(K >> 7) * N - n0) * 2);
+  const auto rsS = make_rsrc(scales + n0, ((uint64_t)(K >> 7) * N - n0) * 2);
+  const auto rsZ = make_rsrc(zeros + n0, ((uint64_t)(K >> 7) * N - n0) * 2);
 
   // A: instruction q covers rows r0 = 8*(A_INSTR*wave + q) .. +7; lane L lands
   // at row r0 + L/8, physical chunk L%8 and so fetches logical chunk
@@ -63,11 +64,26 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
 #pragma unroll
   for (int v = 0; v < 2; ++v)
     a_voff[v] = (uint32_t)((lane >> 3) * K2 + (((lane & 7) ^ (lane >> 3) ^ v) * 16));
-  // B: instruction q covers channels r0 = 32*(2*wave + q) .. +31; lane L lands
-  // at channel r0 + L/2, physical chunk L&1 = logical cc ^ fB(L/2).
-  const int bn = lane >> 1;
-  const int bcc = (lane & 1) ^ (((lane >> 3) ^ (lane >> 4)) & 1);
-  const uint32_t b_voff = (uint32_t)((bn >> 2) * K2 + 32 * (bn & 3) + 16 * bcc);
+  // B: lane (h, l) of channel block j loads 32-k chunk h of channel
+  // n = 64*wave + 32*j + l, i.e. bytes 32*(n&3) + 16*h of the stage's 128-byte
+  // segment of packed row n/4 (one 1 KB instruction covers 8 whole segments);
+  // S / Z: the channel's fp16 scale and scaled zero of the stage's group.
+  uint32_t b_voff[NT], sz_voff[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int n = 64 * wave + 32 * j + l32;
+    b_voff[j] = (uint32_t)((n >> 2) * K2 + 32 * (n & 3) + 16 * h);
+    sz_voff[j] = (uint32_t)(n * 2);
+  }
+  auto load_b = [&](int ks, uint4 (&wq)[NT], uint32_t (&sv)[NT], uint32_t (&zv)[NT]) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      wq[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsB, b_voff[j], ks * 128, 0));
+      sv[j] = __builtin_amdgcn_raw_buffer_load_b16(rsS, sz_voff[j], (ks >> 1) * N * 2, 0);
+      zv[j] = __builtin_amdgcn_raw_buffer_load_b16(rsZ, sz_voff[j], (ks >> 1) * N * 2, 0);
+    }
+  };
+  constexpr int B_INSTR = 3 * NT;               // VMEM instructions of one load_b
 
   const uint32_t lds0 = lds_addr(lds);
   auto issue = [&](int ks, int st) {
@@ -77,14 +93,6 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
       const int r0 = 8 * (A_INSTR * wave + q);
       lds_dma16(rsA, a_voff[(r0 >> 3) & 1], r0 * K2 + ks * 128, base + r0 * 128);
     }
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int r0 = 32 * (2 * wave + q);
-      lds_dma16(rsB, b_voff, (r0 >> 2) * K2 + ks * 128, base + A_BYTES + r0 * 32);
-    }
-    // waves 0,1: the two halves of the scales; waves 2,3: of the scaled zeros
-    lds_dma4(rsS, lane * 4, (ks >> 1) * N * 2 + (wave & 1) * 256,
-             base + A_BYTES + B_BYTES + (wave >> 1) * S_BYTES + (wave & 1) * 256);
   };
 
   f32x16 acc[NT][MT];
@@ -95,14 +103,6 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
-  // per-lane LDS byte offsets that do not depend on the stage
-  uint32_t b_off[NT], s_off[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const int n = 64 * wave + 32 * j + l32;
-    b_off[j] = (uint32_t)(A_BYTES + n * 32 + ((h ^ (((n >> 2) ^ (n >> 3)) & 1)) * 16));
-    s_off[j] = (uint32_t)(A_BYTES + B_BYTES + n * 2);
-  }
   const int fa = (l32 & 7) ^ ((l32 >> 3) & 1);  // fA(32*i + l32) is the same for all i
 
   auto dq = [&](int s, const uint4 (&wq)[NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT], uint4 (&wf)[NT]) {
@@ -120,16 +120,8 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
   // its own MFMAs, then dequantises step s+1's weights (VALU that co-issues
   // with the MFMAs in flight).  The scheduling fences keep the compiler from
   // sinking the reads next to their use, which would expose LDS latency.
-  auto compute = [&](int st) {
+  auto compute = [&](int st, const uint4 (&wq)[NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT]) {
     const uint8_t* base = lds + st * STAGE;
-    uint4 wq[NT];
-    uint32_t sv[NT], zv[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      wq[j] = *reinterpret_cast<const uint4*>(base + b_off[j]);
-      sv[j] = *reinterpret_cast<const uint16_t*>(base + s_off[j]);
-      zv[j] = *reinterpret_cast<const uint16_t*>(base + s_off[j] + S_BYTES);
-    }
     uint4 af[2][MT], wf[2][NT];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -154,27 +146,51 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
     }
   };
 
-  issue(0, 0);
-  if (KS > 1) issue(1, 1);
-  for (int ks = 0; ks < KS; ++ks) {
-    // this wave's loads for stage ks have landed; after the barrier everyone's
-    // have, and every wave is done with stage ks-1 (overwritten next)
-    if (ks + 1 < KS) {
-      __builtin_amdgcn_s_waitcnt(0x0F70 | VM_PER_STAGE);  // vmcnt(VM_PER_STAGE)
-    } else {
-      __builtin_amdgcn_s_waitcnt(0x0F70);                 // vmcnt(0)
-    }
+  // Per stage ks: barrier, B(ks+1) into the idle register set, b_wait, then
+  // A(ks+2), then compute stage ks.  b_wait = vmcnt(B_INSTR) lands everything
+  // issued before B(ks+1): B(ks) and A(ks+1), so the next barrier publishes
+  // every wave's A(ks+1).  The A copies are inline asm the compiler does not
+  // count; waiting right after B(ks+1) is the one place where the hardware
+  // count and the compiler's own count agree that B(ks) is done, so the
+  // compiler adds no wait of its own before stage ks's MFMAs (a wait placed
+  // after A(ks+2) would make it wait, by its count, for loads just issued).
+  // top_wait's vmcnt(A_INSTR + B_INSTR) is a no-op in this order; it keeps
+  // A(ks+1) landed before the barrier however the compiler places the
+  // register loads within a stage.  Past the last stage the loads repeat
+  // stage KS-1 (valid addresses; A into a buffer nobody reads any more, B
+  // into a dead register set), so every iteration issues the same count.
+  static_assert(A_INSTR + B_INSTR < 16, "the vmcnt immediates use the low 4 bits only");
+  auto b_wait = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70 | B_INSTR); };
+  auto top_wait = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (A_INSTR + B_INSTR));
     lds_barrier();
-    if (ks + 2 < KS) issue(ks + 2, (ks + 2) % NSTAGE);
-    compute(ks % NSTAGE);
+  };
+  // B registers alternate between two sets; KS = K / 64 is even (K % 128 == 0)
+  uint4 wq0[NT], wq1[NT];
+  uint32_t sv0[NT], zv0[NT], sv1[NT], zv1[NT];
+  issue(0, 0);
+  load_b(0, wq0, sv0, zv0);
+  issue(1, 1);
+  // lands A(0) wherever the compiler places B(0) relative to A(1)
+  __builtin_amdgcn_s_waitcnt(0x0F70 | A_INSTR);
+  for (int ks = 0; ks < KS; ks += 2) {
+    top_wait();
+    load_b(ks + 1, wq1, sv1, zv1);
+    b_wait();
+    issue(ks + 2 < KS ? ks + 2 : KS - 1, (ks + 2) % NSTAGE);
+    compute(ks % NSTAGE, wq0, sv0, zv0);
+    top_wait();
+    load_b(ks + 2 < KS ? ks + 2 : KS - 1, wq0, sv0, zv0);
+    b_wait();
+    issue(ks + 3 < KS ? ks + 3 : KS - 1, (ks + 3) % NSTAGE);
+    compute((ks + 1) % NSTAGE, wq1, sv1, zv1);
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the repeated loads may not land during the epilogue
 
   // ---- epilogue: the wave's BM x 64 output tile goes through LDS so that the
   // global stores are whole 128-byte rows (direct 8-byte stores from the MFMA
   // layout cost ~3x the output size in HBM write traffic).
   lds_barrier();  // every wave is done reading the pipeline stages
-  constexpr int EP = 144;  // bytes per staged row: 64 fp16 + 16 B pad
-  static_assert(4 * BM * EP <= NSTAGE * STAGE, "epilogue staging fits in the pipeline LDS");
   uint8_t* stg = lds + wave * (BM * EP);
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
