@@ -206,7 +206,9 @@ def gelu_and_quant(x: np.ndarray):
     t32 = tmp.astype(F32)
     zero = F32(F16(0.0001))
     folded = np.where(t32 > zero, t32, -t32)   # act.cu:47-48: not a plain abs
-    amax = np.maximum(folded.max(axis=1), F32(0.0)).astype(F32)
+    # act.cu:49-50: `if ((float)t > amax_val) amax_val = (float)t` from 0, so a
+    # NaN never enters the maximum (fmax skips it)
+    amax = np.fmax.reduce(folded, axis=1, initial=F32(0.0)).astype(F32)
     scale = (amax / F32(127.0)).astype(F32).astype(F16)
     with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
         inv = (F32(127.0) / amax).astype(F32).astype(F16).astype(np.float64)

@@ -137,6 +137,26 @@ def test_gelu_every_finite_fp16_input(gpu):
     assert np.array_equal(q.cpu().numpy(), qr)
 
 
+def test_gelu_non_finite_inputs_match_oracle(gpu):
+    """+-inf and NaN in some rows (others finite), bit for bit against the
+    oracle: the GELU output, the per-row scale and the int8 values."""
+    from qvggt_amd import awq_inference_engine as E
+    x = (_rng(5).standard_normal((5, 1024)) * 2).astype(np.float16)
+    x[0, :3] = [np.inf, -np.inf, np.nan]
+    x[1, 7] = np.inf
+    x[2, 100] = -np.inf
+    x[3, 1023] = np.nan
+    q = torch.empty(x.shape, dtype=torch.int8, device=gpu)
+    s = torch.empty(x.shape[0], dtype=torch.float16, device=gpu)
+    tmp = torch.empty(x.shape, dtype=torch.float16, device=gpu)
+    E.gelu_and_quant(q, torch.from_numpy(x).to(gpu), s, tmp)
+    with np.errstate(over="ignore", invalid="ignore"):
+        qr, sr, tr = Q.gelu_and_quant(x)
+    assert np.array_equal(_bits(tmp), tr.view(np.int16))
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+    assert np.array_equal(q.cpu().numpy(), qr)
+
+
 # ------------------------------------------------------- normalisation
 @pytest.mark.parametrize("shape", [(4, 300, 1024), (2, 7, 4096), (1, 1, 64)])
 def test_layernorm_forward_cuda_rmsnorm_bit_exact(gpu, shape):

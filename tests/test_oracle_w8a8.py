@@ -126,6 +126,28 @@ def test_gelu_and_quant_scale_semantics():
     assert (np.abs(q).max(1) == 127).all()
 
 
+def test_gelu_and_quant_amax_skips_nan_like_the_reference_loop():
+    """act.cu:44-50 keeps amax with `if ((float)t > amax) amax = t` from 0, so a
+    NaN GELU output (from NaN or -inf input) never enters the maximum."""
+    x = np.random.default_rng(9).standard_normal((3, 64)).astype(np.float16)
+    x[0, 5] = np.nan
+    x[1, 9] = -np.inf
+    x[2, 0] = np.inf
+    with np.errstate(over="ignore", invalid="ignore"):
+        q, s, tmp = Q.gelu_and_quant(x)
+    zero = np.float32(np.float16(0.0001))
+    for r in range(3):
+        amax = np.float32(0.0)
+        for t in tmp[r].astype(np.float32):
+            f = t if t > zero else -t
+            if f > amax:
+                amax = f
+        with np.errstate(over="ignore"):
+            want = (amax / np.float32(127)).astype(np.float16)
+        assert s[r].view(np.int16) == want.view(np.int16), r
+    assert np.isnan(tmp[0, 5]) and np.isnan(tmp[1, 9]) and np.isinf(s[2])
+
+
 # ------------------------------------------------------------- GEMM
 def test_w8a8_int32_brute_force_and_epilogue():
     rng = np.random.default_rng(6)
