@@ -78,7 +78,9 @@ def row_sum_f32(v: np.ndarray) -> np.ndarray:
 def quant_per_token(x: np.ndarray):
     """invoke_quant (quantization.cu:42-96): returns (int8 (M,K), fp16 scale (M,))."""
     xf = np.asarray(x).astype(F32)
-    amax = np.abs(xf).max(axis=1).astype(F32)
+    # quantization.cu:49-56: `if (val > amax_val) amax_val = val` from 0, so a
+    # NaN never enters the maximum (fmax skips it)
+    amax = np.fmax.reduce(np.abs(xf), axis=1, initial=F32(0.0)).astype(F32)
     scale = (amax / F32(127.0)).astype(F32).astype(F16)
     with np.errstate(divide="ignore", invalid="ignore"):
         inv = (F32(127.0) / amax).astype(F32)
@@ -132,7 +134,9 @@ def layernorm_quant(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: flo
     t = (t * g).astype(F32)
     t = (t + b).astype(F32)
     y16 = t.astype(F16)
-    amax = np.maximum(np.abs(y16).max(axis=1), F16(1e-6)).astype(F32)
+    # layernorm.cu:103-113: amax = cuda_max(|y|, amax) from 1e-6 in the input
+    # type; that max keeps the non-NaN operand, so NaN never enters it
+    amax = np.fmax.reduce(np.abs(y16), axis=1, initial=F16(1e-6)).astype(F32)
     dyn = (F32(127.0) / amax).astype(F32)
     q = sat_s8((t * dyn[:, None]).astype(F32))
     scale = (amax / F32(127.0)).astype(F32).astype(F16)

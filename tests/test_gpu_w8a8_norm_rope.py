@@ -137,6 +137,30 @@ def test_gelu_every_finite_fp16_input(gpu):
     assert np.array_equal(q.cpu().numpy(), qr)
 
 
+def test_per_token_quant_and_ln_quant_with_nan_rows_match_oracle(gpu):
+    """A NaN element in some rows, bit for bit against the oracle: it stays out
+    of the row maximum (per-token quant) or turns the whole row NaN (LN)."""
+    from qvggt_amd import awq_inference_engine as E
+    x = (_rng(6).standard_normal((4, 1024))).astype(np.float16)
+    x[0, 17] = np.nan
+    x[2, 1000] = np.nan
+    xd = torch.from_numpy(x).to(gpu)
+    q = torch.empty(x.shape, dtype=torch.int8, device=gpu)
+    s = torch.empty(x.shape[0], dtype=torch.float16, device=gpu)
+    E.invoke_quant(q, xd, s)
+    with np.errstate(invalid="ignore"):
+        qr, sr = Q.quant_per_token(x)
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+    assert np.array_equal(q.cpu().numpy(), qr)
+    g = (1 + 0.1 * _rng(7).standard_normal(1024)).astype(np.float16)
+    b = (0.1 * _rng(8).standard_normal(1024)).astype(np.float16)
+    E.rms_norm_general(q, xd, torch.from_numpy(g).to(gpu), torch.from_numpy(b).to(gpu), s, 1e-6, True)
+    with np.errstate(invalid="ignore"):
+        qr, sr = Q.layernorm_quant(x, g, b, 1e-6)
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+    assert np.array_equal(q.cpu().numpy(), qr)
+
+
 def test_gelu_non_finite_inputs_match_oracle(gpu):
     """+-inf and NaN in some rows (others finite), bit for bit against the
     oracle: the GELU output, the per-row scale and the int8 values."""

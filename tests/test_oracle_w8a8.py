@@ -148,6 +148,32 @@ def test_gelu_and_quant_amax_skips_nan_like_the_reference_loop():
     assert np.isnan(tmp[0, 5]) and np.isnan(tmp[1, 9]) and np.isinf(s[2])
 
 
+def test_per_token_amax_skips_nan_like_the_reference_loops():
+    """quantization.cu:49-56 and layernorm.cu:103-113 keep the row maximum with
+    updates that never take a NaN: a NaN element leaves the other rows' and
+    elements' results alone, and a row that is NaN throughout keeps the floor."""
+    x = np.random.default_rng(11).standard_normal((3, 64)).astype(np.float16)
+    x[0, 3] = np.nan
+    with np.errstate(invalid="ignore"):
+        q, s = Q.quant_per_token(x)
+    for r in range(3):
+        amax = np.float32(0.0)
+        for v in np.abs(x[r].astype(np.float32)):
+            if v > amax:
+                amax = v
+        assert s[r].view(np.int16) == (amax / np.float32(127)).astype(np.float16).view(np.int16), r
+    assert q[0, 3] == 0
+    g = np.ones(64, np.float16)
+    b = np.zeros(64, np.float16)
+    with np.errstate(invalid="ignore"):
+        q2, s2 = Q.layernorm_quant(x, g, b, 1e-6)
+    # row 0's mean is NaN, so every y is NaN and amax stays at fp16(1e-6)
+    want0 = (np.float32(np.float16(1e-6)) / np.float32(127)).astype(np.float16)
+    assert s2[0].view(np.int16) == want0.view(np.int16)
+    assert (q2[0] == 0).all()
+    assert np.isfinite(s2[1:].astype(np.float32)).all()
+
+
 # ------------------------------------------------------------- GEMM
 def test_w8a8_int32_brute_force_and_epilogue():
     rng = np.random.default_rng(6)
