@@ -172,6 +172,12 @@ __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
   const int half = j >> 2;
   const int i0 = 8 * (j & 1);
   const bool lo = (j & 2) == 0;
+  // q and k norm weights for this lane's 8 dims, fetched with the rows rather
+  // than after the statistics
+  const f16x8 gqv = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(qg)[j]);
+  const f16x8 bqv = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(qb)[j]);
+  const f16x8 gkv = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(kg)[j]);
+  const f16x8 bkv = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(kb)[j]);
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
     float s = 0.f;
@@ -185,8 +191,8 @@ __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
       s2 = s2 + x[k][e] * x[k][e];
     }
     const float rs = 1.0f / __builtin_sqrtf(sum8_lanes(s2) / 64.0f + eps);
-    const f16x8 g = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(partv[k] ? kg : qg)[j]);
-    const f16x8 b = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(partv[k] ? kb : qb)[j]);
+    const f16x8 g = partv[k] ? gkv : gqv;
+    const f16x8 b = partv[k] ? bkv : bqv;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float t = (x[k][e] * rs) * (float)g[e] + (float)b[e];
