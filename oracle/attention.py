@@ -19,24 +19,26 @@ from __future__ import annotations
 import numpy as np
 
 
-def attention_ref(q, k, v, B: int, L: int, scale: float = 0.125, rows=None) -> np.ndarray:
-    """q, k, v: (B*L, H, D) arrays.  Returns float64 (len(rows) or B*L, H, D)."""
-    q = np.asarray(q, np.float64)
-    k = np.asarray(k, np.float64)
-    v = np.asarray(v, np.float64)
-    T, H, D = q.shape
+def attention_ref(q, k, v, B: int, L: int, scale: float = 0.125, rows=None, q_rows: bool = False) -> np.ndarray:
+    """q, k, v: (B*L, H, D) arrays (``q_rows``: q holds only the selected rows,
+    (len(rows), H, D)).  Returns float64 (len(rows) or B*L, H, D); the
+    products run per head as float64 matrix products."""
+    k = np.asarray(k)
+    v = np.asarray(v)
+    T, H, D = k.shape
     rows = np.arange(T) if rows is None else np.asarray(rows)
+    q = np.asarray(q)
     out = np.empty((len(rows), H, D))
     for seq in range(B):
         sel = np.nonzero((rows >= seq * L) & (rows < (seq + 1) * L))[0]
         if len(sel) == 0:
             continue
-        ks = k[seq * L:(seq + 1) * L]          # (L, H, D)
-        vs = v[seq * L:(seq + 1) * L]
-        qs = q[rows[sel]]                      # (n, H, D)
-        s = np.einsum("nhd,lhd->hnl", qs, ks) * scale
+        ks = np.asarray(k[seq * L:(seq + 1) * L], np.float64).transpose(1, 2, 0)   # (H, D, L)
+        vs = np.asarray(v[seq * L:(seq + 1) * L], np.float64).transpose(1, 0, 2)   # (H, L, D)
+        qs = np.asarray(q[sel] if q_rows else q[rows[sel]], np.float64).transpose(1, 0, 2)  # (H, n, D)
+        s = np.matmul(qs, ks) * scale                                            # (H, n, L)
         s -= s.max(axis=-1, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=-1, keepdims=True)
-        out[sel] = np.einsum("hnl,lhd->nhd", p, vs)
+        out[sel] = np.matmul(p, vs).transpose(1, 0, 2)
     return out

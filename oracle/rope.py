@@ -31,7 +31,9 @@ def cos_sin_f32(theta: np.ndarray):
 
 
 def rope_with_pos(x: np.ndarray, freqs: np.ndarray, out_dtype=None) -> np.ndarray:
-    """x (S, B, H, D) (float array of any float dtype), freqs (B, S, D2) fp32."""
+    """x (S, B, H, D) (float array of any float dtype), freqs (B, S, D2) fp32.
+    ``out_dtype`` "bf16" returns fp32 values rounded to bfloat16 (x then holds
+    bfloat16 values as fp32)."""
     x = np.asarray(x)
     out_dtype = out_dtype or x.dtype
     S, B, H, D = x.shape
@@ -47,6 +49,9 @@ def rope_with_pos(x: np.ndarray, freqs: np.ndarray, out_dtype=None) -> np.ndarra
     out = xf.copy()
     out[..., :half] = first
     out[..., half:D2] = second
+    if isinstance(out_dtype, str) and out_dtype == "bf16":
+        from .w8a8 import round_store
+        return round_store(out, "bf16")
     return out.astype(out_dtype)
 
 

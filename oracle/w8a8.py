@@ -37,8 +37,26 @@ from __future__ import annotations
 
 import numpy as np
 
+from .awq import bf16_bits_to_f32, f64_to_bf16_bits
+
 F32 = np.float32
 F16 = np.float16
+DTYPES = ("f16", "bf16", "f32")
+
+
+def round_store(t, dtype: str = "f16") -> np.ndarray:
+    """fp32 values rounded (nearest even) to a kernel's storage type T and read
+    back as fp32: the ``cuda_cast<T>(...)`` of a float in the reference kernels,
+    which dispatch half, bfloat16 and float (dispatch_utils.h)."""
+    t = np.asarray(t, F32)
+    if dtype == "f16":
+        return t.astype(F16).astype(F32)
+    if dtype == "bf16":
+        with np.errstate(invalid="ignore"):
+            return bf16_bits_to_f32(f64_to_bf16_bits(t.astype(np.float64)))
+    if dtype == "f32":
+        return t
+    raise ValueError(dtype)
 
 
 # --------------------------------------------------------------- rounding
@@ -122,10 +140,12 @@ def _mean_rs_diffsq(xf: np.ndarray, eps: float):
     return mean, rs
 
 
-def layernorm_quant(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float):
+def layernorm_quant(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float, dtype: str = "f16"):
     """rms_norm_general with use_per_token_quant=True (w8a8/layernorm.cu:20-151).
 
-    Returns (int8 (M,D), fp16 scale (M,))."""
+    ``dtype`` is the input's storage type T ("f16", "bf16", "f32"; x, gamma
+    and beta hold values of that type): amax runs over T(y) from a floor of
+    T(1e-6) (layernorm.cu:103-113).  Returns (int8 (M,D), fp16 scale (M,))."""
     xf = np.asarray(x).astype(F32)
     g = np.asarray(gamma).astype(F32)[None, :]
     b = np.asarray(beta).astype(F32)[None, :]
@@ -133,37 +153,45 @@ def layernorm_quant(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: flo
     t = ((xf - mean[:, None]).astype(F32) * rs[:, None]).astype(F32)
     t = (t * g).astype(F32)
     t = (t + b).astype(F32)
-    y16 = t.astype(F16)
+    yT = round_store(t, dtype)
     # layernorm.cu:103-113: amax = cuda_max(|y|, amax) from 1e-6 in the input
     # type; that max keeps the non-NaN operand, so NaN never enters it
-    amax = np.fmax.reduce(np.abs(y16), axis=1, initial=F16(1e-6)).astype(F32)
+    floor = round_store(np.array([1e-6], F32), dtype)[0]
+    amax = np.fmax.reduce(np.abs(yT), axis=1, initial=floor).astype(F32)
     dyn = (F32(127.0) / amax).astype(F32)
     q = sat_s8((t * dyn[:, None]).astype(F32))
     scale = (amax / F32(127.0)).astype(F32).astype(F16)
     return q, scale
 
 
-def layernorm_quant_per_tensor(x, gamma, eps, scale_fp16):
-    """rms_norm_general with use_per_token_quant=False (layernorm.cu:119-123):
-    no beta, int8 = sat(rint(fp32(fp16(LN)) * float(scale)))."""
+def layernorm_quant_per_tensor(x, gamma, eps, scale_fp16, dtype: str = "f16"):
+    """rms_norm_general with use_per_token_quant=False (layernorm.cu:100-123,
+    host layernorm.cu:180-187 passes beta = nullptr): no beta,
+    int8 = sat(rint(float(T(LN * gamma)) * float(scale))), T the input's
+    storage type, scale the fp16 per-tensor scale."""
     xf = np.asarray(x).astype(F32)
     g = np.asarray(gamma).astype(F32)[None, :]
     mean, rs = _mean_rs_diffsq(xf, eps)
     t = ((xf - mean[:, None]).astype(F32) * rs[:, None]).astype(F32)
     t = (t * g).astype(F32)
-    y16 = t.astype(F16).astype(F32)
-    return sat_s8((y16 * F32(np.float16(scale_fp16))).astype(F32))
+    yT = round_store(t, dtype)
+    return sat_s8((yT * F32(np.float16(scale_fp16))).astype(F32))
 
 
-def rmsnorm(x: np.ndarray, gamma: np.ndarray, eps: float) -> np.ndarray:
-    """T5 RMSNorm (layernorm/layernorm.cu:31-57): clamp((x * rs) * g) -> fp16."""
+def rmsnorm(x: np.ndarray, gamma: np.ndarray, eps: float, dtype: str = "f16") -> np.ndarray:
+    """T5 RMSNorm (layernorm/layernorm.cu:31-57): (x * rs) * g, for half
+    clamped to +-(65504 - 1000) before the conversion (reduction.cuh:60-71,
+    clamp_inf_for_half; the bfloat16 instantiation converts unclamped).
+    Returns fp16 for dtype "f16", else fp32 values of the storage type."""
     xf = np.asarray(x).astype(F32)
     D = xf.shape[1]
     s2 = row_sum_f32((xf * xf).astype(F32))
     rs = (F32(1.0) / np.sqrt(((s2 / F32(D)).astype(F32) + F32(eps)).astype(F32))).astype(F32)
     t = ((xf * rs[:, None]).astype(F32) * np.asarray(gamma).astype(F32)[None, :]).astype(F32)
-    t = np.clip(t, F32(-65504.0 + 1000.0), F32(65504.0 - 1000.0))
-    return t.astype(F16)
+    if dtype == "f16":
+        t = np.clip(t, F32(-65504.0 + 1000.0), F32(65504.0 - 1000.0))
+        return t.astype(F16)
+    return round_store(t, dtype)
 
 
 def layernorm(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float = 1e-6) -> np.ndarray:

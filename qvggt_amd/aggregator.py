@@ -20,8 +20,9 @@ reference's loader uses for the quantised layers
 Assumptions taken from the public VGGT design where the reference and the
 benchmark configs are silent: qk-norm on, LayerScale init 0.01 (AA blocks) and
 1e-5 (DINOv2), exact-erf GELU in the W4 path (the W8A8 path uses the
-reference's tanh gelu_and_quant), LayerNorm eps 1e-6 (the benchmark
-configuration's LayerNorm(1024, eps 1e-6)) in the AA blocks and DINOv2.
+reference's tanh gelu_and_quant).  LayerNorm eps, depth and the RoPE base
+come from ``AggregatorConfig`` (a checkpoint's config.json); its defaults are
+the benchmark configuration's LayerNorm(1024, eps 1e-6) and 24 + 24 blocks.
 
 Every hot op runs on libqvggt_hip.so; only the DINOv2 fp16 linears (plain
 GEMMs: hipBLASLt through torch), its GELU, the patch convolution and the
@@ -29,7 +30,10 @@ LayerScale residual updates use torch.
 """
 from __future__ import annotations
 
+import dataclasses
+import json
 import math
+from pathlib import Path
 
 import numpy as np
 import torch
@@ -51,9 +55,89 @@ N_REG = 4
 SPECIALS = 1 + N_REG         # camera + registers
 TOKENS = SPECIALS + GRID * GRID   # 1374
 DEPTH = 24
-LN_EPS = 1e-6                 # DINOv2 patch-embed LayerNorms
-BLOCK_LN_EPS = 1e-6           # AA-block norm1 / norm2 / q_norm / k_norm
+LN_EPS = 1e-6                 # default DINOv2 patch-embed LayerNorm eps
+BLOCK_LN_EPS = 1e-6           # default AA-block norm1 / norm2 / q_norm / k_norm eps
 HEAD_LAYERS = (4, 11, 17, 23)     # intermediate outputs VGGT's heads consume
+
+
+@dataclasses.dataclass(frozen=True)
+class AggregatorConfig:
+    """Model parameters of the aggregator, read from the checkpoint's model
+    config as the reference builds its model from ``VGGTConfig`` (loader.py:146-162:
+    ``VGGTConfig.from_pretrained(dirname(model_path))``, defaults otherwise).
+
+    The defaults are the benchmark configuration (
+    LayerNorm(1024, eps 1e-6), 24 + 24 blocks).  VGGT's published blocks build
+    their norms with torch's default eps 1e-5, so a real checkpoint's config
+    decides.  The kernels fix dim 1024, 16 heads of 64, MLP 4096 and the
+    37 x 37 patch grid; other values are refused."""
+    depth: int = DEPTH                 # AA iterations (one frame + one global block each)
+    block_ln_eps: float = BLOCK_LN_EPS  # norm1 / norm2 / q_norm / k_norm of the AA blocks
+    dino_depth: int = DEPTH            # DINOv2 patch-embed blocks
+    dino_ln_eps: float = LN_EPS        # DINOv2 norms
+    embed_dim: int = DIM
+    num_heads: int = HEADS
+    mlp_dim: int = MLP_DIM
+    patch_size: int = PATCH
+    img_size: int = IMG
+    num_register_tokens: int = N_REG
+    rope_base: float = 100.0
+
+    # config.json keys accepted for each field (the vggt-hf VGGTConfig is
+    # external and unpinned, so common Hugging Face spellings are all read)
+    _ALIASES = {
+        "depth": ("aa_depth", "depth", "num_hidden_layers"),
+        "block_ln_eps": ("aa_layer_norm_eps", "block_layer_norm_eps", "layer_norm_eps", "norm_eps"),
+        "dino_depth": ("patch_embed_depth", "dino_depth"),
+        "dino_ln_eps": ("patch_embed_layer_norm_eps", "dino_layer_norm_eps"),
+        "embed_dim": ("embed_dim", "hidden_size"),
+        "num_heads": ("num_heads", "num_attention_heads"),
+        "mlp_dim": ("mlp_dim", "intermediate_size"),
+        "patch_size": ("patch_size",),
+        "img_size": ("img_size", "image_size"),
+        "num_register_tokens": ("num_register_tokens",),
+        "rope_base": ("rope_freq", "rope_theta", "rope_base"),
+    }
+
+    def __post_init__(self):
+        fixed = dict(embed_dim=DIM, num_heads=HEADS, mlp_dim=MLP_DIM, patch_size=PATCH, img_size=IMG,
+                     num_register_tokens=N_REG)
+        bad = {k: getattr(self, k) for k, v in fixed.items() if getattr(self, k) != v}
+        if bad:
+            raise ValueError(f"AggregatorConfig: unsupported model parameters {bad} (the kernels are built for {fixed})")
+        if self.depth < 1 or self.dino_depth < 0 or not (self.block_ln_eps >= 0 and self.dino_ln_eps >= 0):
+            raise ValueError(f"AggregatorConfig: bad depth / eps in {self}")
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "AggregatorConfig":
+        """Fields from a model-config dict (nested ``aggregator`` /
+        ``patch_embed`` sections are searched too); missing keys keep their
+        defaults, and ``mlp_ratio`` gives ``mlp_dim``."""
+        flat = dict(d)
+        for sec in ("aggregator_config", "aggregator", "patch_embed_config"):
+            if isinstance(d.get(sec), dict):
+                flat.update(d[sec])
+        kw = {}
+        for field, keys in cls._ALIASES.items():
+            for k in keys:
+                if k in flat and flat[k] is not None:
+                    kw[field] = type(getattr(cls(), field))(flat[k])
+                    break
+        if "mlp_dim" not in kw and flat.get("mlp_ratio") is not None:
+            kw["mlp_dim"] = int(round(float(flat["mlp_ratio"]) * kw.get("embed_dim", DIM)))
+        return cls(**kw)
+
+    @classmethod
+    def from_pretrained(cls, path) -> "AggregatorConfig":
+        """``config.json`` of a checkpoint directory (or of the directory of a
+        checkpoint file), read as JSON; defaults when there is none."""
+        p = Path(path)
+        cfg = (p if p.is_dir() else p.parent) / "config.json"
+        if not cfg.exists():
+            return cls()
+        return cls.from_dict(json.loads(cfg.read_text()))
+
+
 IMAGENET_MEAN = (0.485, 0.456, 0.406)
 IMAGENET_STD = (0.229, 0.224, 0.225)
 
@@ -145,6 +229,10 @@ def _linear(layer, x: torch.Tensor, epilogue: int, out: torch.Tensor) -> torch.T
     return y
 
 
+def _with_depth(cfg: AggregatorConfig, depth: int | None) -> AggregatorConfig:
+    return cfg if depth is None else dataclasses.replace(cfg, depth=depth, dino_depth=depth)
+
+
 # ------------------------------------------------------------------ blocks
 class LayerScale(nn.Module):
     def __init__(self, dim, init, dev=None):
@@ -153,11 +241,11 @@ class LayerScale(nn.Module):
 
 
 class AAAttention(nn.Module):
-    def __init__(self, qkv, proj, dev=None):
+    def __init__(self, qkv, proj, dev=None, eps: float = BLOCK_LN_EPS):
         super().__init__()
         self.qkv, self.proj = qkv, proj
-        self.q_norm = nn.LayerNorm(HEAD_DIM, eps=BLOCK_LN_EPS, device=dev, dtype=torch.float16)
-        self.k_norm = nn.LayerNorm(HEAD_DIM, eps=BLOCK_LN_EPS, device=dev, dtype=torch.float16)
+        self.q_norm = nn.LayerNorm(HEAD_DIM, eps=eps, device=dev, dtype=torch.float16)
+        self.k_norm = nn.LayerNorm(HEAD_DIM, eps=eps, device=dev, dtype=torch.float16)
 
 
 class Mlp(nn.Module):
@@ -170,13 +258,14 @@ class AABlock(nn.Module):
     """Frame or global block with W4A16 (``WQLinear``) or W8A8 linears; in the
     W4 form any of the four linears may also be an fp16 ``nn.Linear``."""
 
-    def __init__(self, qkv, proj, fc1, fc2, w8a8: bool, dev=None):
+    def __init__(self, qkv, proj, fc1, fc2, w8a8: bool, dev=None, eps: float = BLOCK_LN_EPS):
         super().__init__()
         self.w8a8 = w8a8
-        self.norm1 = nn.LayerNorm(DIM, eps=BLOCK_LN_EPS, device=dev, dtype=torch.float16)
-        self.attn = AAAttention(qkv, proj, dev)
+        self.eps = float(eps)
+        self.norm1 = nn.LayerNorm(DIM, eps=eps, device=dev, dtype=torch.float16)
+        self.attn = AAAttention(qkv, proj, dev, eps)
         self.ls1 = LayerScale(DIM, 0.01, dev)
-        self.norm2 = nn.LayerNorm(DIM, eps=BLOCK_LN_EPS, device=dev, dtype=torch.float16)
+        self.norm2 = nn.LayerNorm(DIM, eps=eps, device=dev, dtype=torch.float16)
         self.mlp = Mlp(fc1, fc2)
         self.ls2 = LayerScale(DIM, 0.01, dev)
 
@@ -185,14 +274,15 @@ class AABlock(nn.Module):
         """x: (M, 1024) fp16, updated in place.  ws: scratch buffers keyed by name."""
         M = x.shape[0]
         a = self.attn
+        eps = self.eps
         if not self.w8a8:
-            h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, BLOCK_LN_EPS, out=ws["h"])
+            h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, eps, out=ws["h"])
             qkv = _linear(a.qkv, h, QV_EPI_BIAS, ws["qkv"])
         else:
-            E.rms_norm_general(ws["q8"], x, self.norm1.weight, self.norm1.bias, ws["s8"], BLOCK_LN_EPS, True)
+            E.rms_norm_general(ws["q8"], x, self.norm1.weight, self.norm1.bias, ws["s8"], eps, True)
             qkv = a.qkv(ws["q8"], ws["s8"], out=ws["qkv"])
         E.qknorm_rope2d(qkv, pos, tables[0], tables[1], HEADS, a.q_norm.weight, a.q_norm.bias,
-                        a.k_norm.weight, a.k_norm.bias, BLOCK_LN_EPS)
+                        a.k_norm.weight, a.k_norm.bias, eps)
         v3 = qkv.view(M, 3, HEADS, HEAD_DIM)
         att = E.attention(v3[:, 0], v3[:, 1], v3[:, 2], seq_len, out=ws["att"].view(M, HEADS, HEAD_DIM))
         att = att.view(M, DIM)
@@ -204,11 +294,11 @@ class AABlock(nn.Module):
             x.addcmul_(o, self.ls1.gamma)
         m = self.mlp
         if not self.w8a8:
-            h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, BLOCK_LN_EPS, out=ws["h"])
+            h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, eps, out=ws["h"])
             f = _linear(m.fc1, h, QV_EPI_BIAS_GELU, ws["f"])
             _linear_residual(m.fc2, f, self.ls2.gamma, x, ws["o"])
         else:
-            E.rms_norm_general(ws["q8"], x, self.norm2.weight, self.norm2.bias, ws["s8"], BLOCK_LN_EPS, True)
+            E.rms_norm_general(ws["q8"], x, self.norm2.weight, self.norm2.bias, ws["s8"], eps, True)
             f = m.fc1(ws["q8"], ws["s8"], out=ws["f"])
             E.gelu_and_quant(ws["q8f"], f, ws["s8"], ws["ftmp"])
             o = m.fc2(ws["q8f"], ws["s8"], out=ws["o"])
@@ -219,28 +309,29 @@ class AABlock(nn.Module):
 class DinoBlock(nn.Module):
     """DINOv2 ViT-L block in fp16 (linears through hipBLASLt, LN/attention on our kernels)."""
 
-    def __init__(self, dev=None):
+    def __init__(self, dev=None, eps: float = LN_EPS):
         super().__init__()
         kw = dict(device=dev, dtype=torch.float16)
-        self.norm1 = nn.LayerNorm(DIM, eps=LN_EPS, **kw)
+        self.eps = float(eps)
+        self.norm1 = nn.LayerNorm(DIM, eps=eps, **kw)
         self.attn = nn.Module()
         self.attn.qkv = nn.Linear(DIM, 3 * DIM, **kw)
         self.attn.proj = nn.Linear(DIM, DIM, **kw)
         self.ls1 = LayerScale(DIM, 1e-5, dev)
-        self.norm2 = nn.LayerNorm(DIM, eps=LN_EPS, **kw)
+        self.norm2 = nn.LayerNorm(DIM, eps=eps, **kw)
         self.mlp = Mlp(nn.Linear(DIM, MLP_DIM, **kw), nn.Linear(MLP_DIM, DIM, **kw))
         self.ls2 = LayerScale(DIM, 1e-5, dev)
 
     @torch.no_grad()
     def forward(self, x: torch.Tensor, ws: dict) -> torch.Tensor:
         M = x.shape[0]
-        h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, LN_EPS, out=ws["h"])
+        h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, self.eps, out=ws["h"])
         qkv = torch.addmm(self.attn.qkv.bias, h, self.attn.qkv.weight.t(), out=ws["qkv"])
         v3 = qkv.view(M, 3, HEADS, HEAD_DIM)
         att = E.attention(v3[:, 0], v3[:, 1], v3[:, 2], TOKENS, out=ws["att"].view(M, HEADS, HEAD_DIM))
         o = torch.addmm(self.attn.proj.bias, att.view(M, DIM), self.attn.proj.weight.t(), out=ws["o"])
         x.addcmul_(o, self.ls1.gamma)
-        h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, LN_EPS, out=ws["h"])
+        h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, self.eps, out=ws["h"])
         f = torch.addmm(self.mlp.fc1.bias, h, self.mlp.fc1.weight.t(), out=ws["f"])
         f = F.gelu(f)
         o = torch.addmm(self.mlp.fc2.bias, f, self.mlp.fc2.weight.t(), out=ws["o"])
@@ -251,16 +342,17 @@ class DinoBlock(nn.Module):
 class DinoPatchEmbed(nn.Module):
     """DINOv2 ViT-L/14 with 4 registers; returns the normalised patch tokens."""
 
-    def __init__(self, dev=None, depth: int = DEPTH):
+    def __init__(self, dev=None, depth: int = DEPTH, eps: float = LN_EPS):
         super().__init__()
         kw = dict(device=dev, dtype=torch.float16)
+        self.eps = float(eps)
         self.patch_embed = nn.Module()
         self.patch_embed.proj = nn.Conv2d(3, DIM, PATCH, PATCH, **kw)
         self.cls_token = nn.Parameter(torch.zeros(1, 1, DIM, **kw), requires_grad=False)
         self.register_tokens = nn.Parameter(torch.zeros(1, N_REG, DIM, **kw), requires_grad=False)
         self.pos_embed = nn.Parameter(torch.zeros(1, 1 + GRID * GRID, DIM, **kw), requires_grad=False)
-        self.blocks = nn.ModuleList([DinoBlock(dev) for _ in range(depth)])
-        self.norm = nn.LayerNorm(DIM, eps=LN_EPS, **kw)
+        self.blocks = nn.ModuleList([DinoBlock(dev, eps) for _ in range(depth)])
+        self.norm = nn.LayerNorm(DIM, eps=eps, **kw)
 
     @torch.no_grad()
     def forward(self, images: torch.Tensor, ws: dict) -> torch.Tensor:
@@ -273,7 +365,7 @@ class DinoPatchEmbed(nn.Module):
         x = x.view(S * TOKENS, DIM)
         for blk in self.blocks:
             blk(x, ws)
-        return E.layer_norm(x, self.norm.weight, self.norm.bias, LN_EPS).view(S, TOKENS, DIM)[:, SPECIALS:]
+        return E.layer_norm(x, self.norm.weight, self.norm.bias, self.eps).view(S, TOKENS, DIM)[:, SPECIALS:]
 
 
 class Aggregator(nn.Module):
@@ -285,10 +377,11 @@ class Aggregator(nn.Module):
     (S*1374, 1024) plus the per-layer [frame | global] outputs VGGT's heads use.
     """
 
-    def __init__(self, frame_blocks, global_blocks, w8a8: bool, dev=None, dino_depth: int = DEPTH):
+    def __init__(self, frame_blocks, global_blocks, w8a8: bool, dev=None, config: AggregatorConfig | None = None):
         super().__init__()
+        self.config = config or AggregatorConfig(depth=len(frame_blocks))
         self.w8a8 = w8a8
-        self.patch_embed = DinoPatchEmbed(dev, dino_depth)
+        self.patch_embed = DinoPatchEmbed(dev, self.config.dino_depth, self.config.dino_ln_eps)
         self.camera_token = nn.Parameter(torch.zeros(1, 2, 1, DIM, dtype=torch.float16, device=dev),
                                          requires_grad=False)
         self.register_token = nn.Parameter(torch.zeros(1, 2, N_REG, DIM, dtype=torch.float16, device=dev),
@@ -303,25 +396,32 @@ class Aggregator(nn.Module):
     # ---------------------------------------------------------- construction
     @classmethod
     @torch.no_grad()
-    def empty(cls, device="cuda", depth: int = DEPTH):
+    def empty(cls, device="cuda", depth: int | None = None, config: AggregatorConfig | None = None):
         """fp16 aggregator with zero weights and plain ``nn.Linear`` AA linears,
         the starting point of checkpoint loading (qvggt_amd.loader swaps the
-        quantised layers for ``WQLinear`` before the state dict goes in)."""
+        quantised layers for ``WQLinear`` before the state dict goes in).
+        ``depth`` overrides both depths of ``config``."""
+        cfg = _with_depth(config or AggregatorConfig(), depth)
         dev = torch.device(device)
 
         def lin(k, n):
             return nn.Linear(k, n, device=dev, dtype=torch.float16)
 
         def block():
-            return AABlock(lin(DIM, 3 * DIM), lin(DIM, DIM), lin(DIM, MLP_DIM), lin(MLP_DIM, DIM), False, dev)
+            return AABlock(lin(DIM, 3 * DIM), lin(DIM, DIM), lin(DIM, MLP_DIM), lin(MLP_DIM, DIM), False, dev,
+                           cfg.block_ln_eps)
 
-        return cls([block() for _ in range(depth)], [block() for _ in range(depth)], False, dev, dino_depth=depth)
+        return cls([block() for _ in range(cfg.depth)], [block() for _ in range(cfg.depth)], False, dev, cfg)
 
     @classmethod
     @torch.no_grad()
-    def random(cls, w8a8: bool = False, seed: int = 0, device="cuda", depth: int = DEPTH):
+    def random(cls, w8a8: bool = False, seed: int = 0, device="cuda", depth: int | None = None,
+               config: AggregatorConfig | None = None, layerscale: float = 0.01):
         """Seeded random-init weights (trunc-normal-like N(0, 0.02) linears), the
-        AA linears quantised to W4 g128 (default) or W8A8."""
+        AA linears quantised to W4 g128 (default) or W8A8; AA LayerScale
+        ``layerscale`` (VGGT's init value 0.01 by default).  ``depth``
+        overrides both depths of ``config``."""
+        cfg = _with_depth(config or AggregatorConfig(), depth)
         dev = torch.device(device)
         g = torch.Generator(device=dev).manual_seed(seed)
 
@@ -335,7 +435,10 @@ class Aggregator(nn.Module):
             return W8A8Linear.from_linear(l) if w8a8 else quantize_w4(l)
 
         def block():
-            b = AABlock(q(lin(DIM, 3 * DIM)), q(lin(DIM, DIM)), q(lin(DIM, MLP_DIM)), q(lin(MLP_DIM, DIM)), w8a8, dev)
+            b = AABlock(q(lin(DIM, 3 * DIM)), q(lin(DIM, DIM)), q(lin(DIM, MLP_DIM)), q(lin(MLP_DIM, DIM)), w8a8, dev,
+                        cfg.block_ln_eps)
+            b.ls1.gamma.fill_(layerscale)
+            b.ls2.gamma.fill_(layerscale)
             for ln in (b.norm1, b.norm2):
                 ln.weight.copy_((1 + 0.1 * torch.randn(DIM, generator=g, device=dev)).half())
                 ln.bias.copy_((0.1 * torch.randn(DIM, generator=g, device=dev)).half())
@@ -344,9 +447,9 @@ class Aggregator(nn.Module):
                 ln.bias.copy_((0.1 * torch.randn(HEAD_DIM, generator=g, device=dev)).half())
             return b
 
-        frame = [block() for _ in range(depth)]
-        glob = [block() for _ in range(depth)]
-        agg = cls(frame, glob, w8a8, dev, dino_depth=depth)
+        frame = [block() for _ in range(cfg.depth)]
+        glob = [block() for _ in range(cfg.depth)]
+        agg = cls(frame, glob, w8a8, dev, cfg)
         pe = agg.patch_embed
         pe.patch_embed.proj.weight.copy_((torch.randn(pe.patch_embed.proj.weight.shape, generator=g, device=dev) * 0.02).half())
         pe.patch_embed.proj.bias.zero_()
@@ -392,7 +495,7 @@ class Aggregator(nn.Module):
         M = S * TOKENS
         ws = self._workspace(M, dev)
         if self._tables is None or self._tables[0].device != dev:
-            self._tables = E.rope2d_tables(GRID + 1, 100.0, device=dev)
+            self._tables = E.rope2d_tables(GRID + 1, self.config.rope_base, device=dev)
         pos = vggt_positions(S, dev)
         x_img = (images - self.img_mean) / self.img_std
         patches = self.patch_embed(x_img, ws)                                   # (S, 1369, D)

@@ -85,7 +85,38 @@ def _device(dev: torch.device):
 
 
 def _contig(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous view or copy.  A copy must be bound to a name that lives until
+    the native call returns: passing ``_ptr(_contig(t))`` would hand the kernel
+    the address of a temporary that the caching allocator may already have
+    given to the next argument's copy."""
     return t if t.is_contiguous() else t.contiguous()
+
+
+def _contig_opt(t: torch.Tensor | None) -> torch.Tensor | None:
+    return None if t is None else _contig(t)
+
+
+def _check_out(out: torch.Tensor, M: int, N: int, dtype, what: str):
+    """A caller-provided GEMM output: (..., N) with M*N elements, the input's
+    dtype, contiguous, 16-byte aligned (the epilogue stores 16-byte rows)."""
+    if not isinstance(out, torch.Tensor) or out.dtype != dtype:
+        _fail(f"{what}: out must be a {dtype} tensor")
+    if out.dim() < 1 or out.shape[-1] != N or out.numel() != M * N or not out.is_contiguous():
+        _fail(f"{what}: out must be a contiguous (..., {N}) tensor of {M} x {N} elements, "
+              f"got {tuple(out.shape)}")
+    if out.data_ptr() % 16:
+        _fail(f"{what}: out must be 16-byte aligned")
+
+
+def _check_rope_tables(cos_table: torch.Tensor, sin_table: torch.Tensor, what: str):
+    """2-D RoPE tables: contiguous float32 (P, 16), both the same shape (the
+    kernels read row p at p*16, p clamped to P-1)."""
+    for t in (cos_table, sin_table):
+        if (not isinstance(t, torch.Tensor) or t.dtype != torch.float32 or t.dim() != 2
+                or t.shape[1] != 16 or t.shape[0] < 1 or not t.is_contiguous()):
+            _fail(f"{what}: tables must be contiguous float32 (P, 16)")
+    if cos_table.shape != sin_table.shape:
+        _fail(f"{what}: cos and sin tables differ in shape")
 
 
 def _check_w4_tables(kernel, scales, zeros, N, K, dt, what):
@@ -108,24 +139,29 @@ def w4a16_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
                  epilogue: int = QV_EPI_NONE, out: torch.Tensor | None = None) -> torch.Tensor:
     """W4A16 g128 linear with an optional fused epilogue (bias, bias+GELU).
 
-    Routes M <= 16 to the wavefront-reduction GEMV kernel and larger M to the
-    MFMA GEMM.  Used by ``WQLinear`` to fuse qmodule.py:367's bias add.
+    Routes M <= 16 to the GEMV entry and larger M to the GEMM entry; both run
+    every M <= 64 on the skinny-M MFMA kernel.  Used by ``WQLinear`` to fuse
+    qmodule.py:367's bias add.  ``out``, when given, must be a contiguous,
+    16-byte aligned (..., N) tensor of the input's dtype.
     """
     what = "w4a16_linear"
-    dev = _on_gpu(x, qweight, scales, scaled_zeros, bias, what=what)
     dt = _dtype_code(x, what)
-    x = _contig(x)
     K = x.shape[-1]
     M = x.numel() // K if K else 0
     N = qweight.shape[0] * 4
     _check_w4_tables(qweight, scales, scaled_zeros, N, K, x.dtype, what)
     if bias is not None and (bias.dtype != x.dtype or bias.numel() != N):
         _fail(f"{what}: bias must be ({N},) {x.dtype}")
+    if out is not None:
+        _check_out(out, M, N, x.dtype, what)
+    dev = _on_gpu(x, qweight, scales, scaled_zeros, bias, out, what=what)
+    x = _contig(x)
     if out is None:
         out = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=dev)
+    # contiguous copies bound to names: they must outlive the native call
+    qw, sc, sz, bb = _contig(qweight), _contig(scales), _contig(scaled_zeros), _contig_opt(bias)
     with _device(dev):
-        args = (_ptr(x), _ptr(_contig(qweight)), _ptr(_contig(scales)), _ptr(_contig(scaled_zeros)),
-                _ptr(bias), _ptr(out))
+        args = (_ptr(x), _ptr(qw), _ptr(sc), _ptr(sz), _ptr(bb), _ptr(out))
         if 1 <= M <= 16:
             _lib.call("qv_w4a16_gemv", *args, M, N, K, GROUP_SIZE, dt, epilogue, _stream(dev))
         else:
@@ -152,10 +188,11 @@ def w4a16_linear_residual(x: torch.Tensor, qweight: torch.Tensor, scales: torch.
             _fail(f"{what}: {name} must be ({N},) {x.dtype}")
     if residual.dtype != x.dtype or residual.numel() != M * N or not residual.is_contiguous():
         _fail(f"{what}: residual must be a contiguous {x.dtype} tensor of {M} x {N} elements")
+    qw, sc, sz = _contig(qweight), _contig(scales), _contig(scaled_zeros)
+    bb, gg = _contig(bias), _contig(gamma)
     with _device(dev):
-        _lib.call("qv_w4a16_gemm_residual", _ptr(x), _ptr(_contig(qweight)), _ptr(_contig(scales)),
-                  _ptr(_contig(scaled_zeros)), _ptr(_contig(bias)), _ptr(_contig(gamma)), _ptr(residual),
-                  M, N, K, dt, _stream(dev))
+        _lib.call("qv_w4a16_gemm_residual", _ptr(x), _ptr(qw), _ptr(sc), _ptr(sz), _ptr(bb), _ptr(gg),
+                  _ptr(residual), M, N, K, dt, _stream(dev))
     return residual
 
 
@@ -176,10 +213,10 @@ def gemm_forward_cuda_new(in_feats: torch.Tensor, kernel: torch.Tensor, scales: 
     out = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=dev)
     if M == 0:
         return out
+    qw, sc, sz = _contig(kernel), _contig(scales), _contig(zeros)
     with _device(dev):
-        _lib.call("qv_w4a16_gemm", _ptr(x), _ptr(_contig(kernel)), _ptr(_contig(scales)),
-                  _ptr(_contig(zeros)), C.c_void_p(0), _ptr(out), M, N, K, dt, QV_EPI_NONE,
-                  _stream(dev))
+        _lib.call("qv_w4a16_gemm", _ptr(x), _ptr(qw), _ptr(sc), _ptr(sz), C.c_void_p(0), _ptr(out),
+                  M, N, K, dt, QV_EPI_NONE, _stream(dev))
     return out
 
 
@@ -197,16 +234,19 @@ def gemv_forward_cuda_new(in_feats: torch.Tensor, kernel: torch.Tensor,
         _fail("Unsupported group size for gemv kernel.")
     if not 1 <= m <= 7:
         _fail("Unsupported batch size for gemv kernel.")
-    if in_feats.numel() != m * k:
-        _fail(f"{what}: in_feats has {in_feats.numel()} elements, expected m*k = {m * k}")
+    if in_feats.dim() < 1 or in_feats.shape[-1] != k or in_feats.numel() != m * k:
+        _fail(f"{what}: in_feats must be (..., k = {k}) with m*k = {m * k} elements, "
+              f"got {tuple(in_feats.shape)}")
+    if kernel.dim() != 2 or kernel.shape[0] * 4 != n:
+        _fail(f"{what}: kernel must be (n/4, k) = ({n // 4}, {k}), got {tuple(kernel.shape)}")
     _check_w4_tables(kernel, scaling_factors, zeros, n, k, in_feats.dtype, what)
     dev = _on_gpu(in_feats, kernel, scaling_factors, zeros, what=what)
     x = _contig(in_feats)
     out = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
+    qw, sc, sz = _contig(kernel), _contig(scaling_factors), _contig(zeros)
     with _device(dev):
-        _lib.call("qv_w4a16_gemv", _ptr(x), _ptr(_contig(kernel)), _ptr(_contig(scaling_factors)),
-                  _ptr(_contig(zeros)), C.c_void_p(0), _ptr(out), m, n, k, group_size, dt,
-                  QV_EPI_NONE, _stream(dev))
+        _lib.call("qv_w4a16_gemv", _ptr(x), _ptr(qw), _ptr(sc), _ptr(sz), C.c_void_p(0), _ptr(out),
+                  m, n, k, group_size, dt, QV_EPI_NONE, _stream(dev))
     return out
 
 
@@ -220,9 +260,9 @@ def w4a16_dequantize(kernel: torch.Tensor, scales: torch.Tensor, zeros: torch.Te
     N = kernel.shape[0] * 4
     _check_w4_tables(kernel, scales, zeros, N, K, scales.dtype, what)
     out = torch.empty(N, K, dtype=scales.dtype, device=dev)
+    qw, sc, sz = _contig(kernel), _contig(scales), _contig(zeros)
     with _device(dev):
-        _lib.call("qv_w4a16_dequant", _ptr(_contig(kernel)), _ptr(_contig(scales)),
-                  _ptr(_contig(zeros)), _ptr(out), N, K, dt, _stream(dev))
+        _lib.call("qv_w4a16_dequant", _ptr(qw), _ptr(sc), _ptr(sz), _ptr(out), N, K, dt, _stream(dev))
     return out
 
 
@@ -253,9 +293,10 @@ def w4a16_pack(weight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
     qweight = torch.empty(N // 4, K, dtype=torch.int16, device=dev)
     s_out = torch.empty(rows, N, dtype=weight.dtype, device=dev)
     sz_out = torch.empty(rows, N, dtype=weight.dtype, device=dev)
+    w, s, z = _contig(weight), _contig(scales), _contig(zeros)
     with _device(dev):
-        _lib.call("qv_w4a16_pack", _ptr(_contig(weight)), _ptr(_contig(scales)), _ptr(_contig(zeros)),
-                  _ptr(qweight), _ptr(s_out), _ptr(sz_out), N, K, group_size, dt, _stream(dev))
+        _lib.call("qv_w4a16_pack", _ptr(w), _ptr(s), _ptr(z), _ptr(qweight), _ptr(s_out), _ptr(sz_out),
+                  N, K, group_size, dt, _stream(dev))
     return qweight, s_out, sz_out
 
 
@@ -394,10 +435,10 @@ def rms_norm_general(out: torch.Tensor, input: torch.Tensor, weight: torch.Tenso
     if out.numel() != input.numel() or scaling.numel() < (M if use_per_token_quant else 1):
         _fail(f"{what}: out must match input; scaling too small")
     dev = _on_gpu(out, input, weight, bias if use_per_token_quant else None, scaling, what=what)
-    x = _contig(input)
+    x, w = _contig(input), _contig(weight)
+    b = _contig(bias) if use_per_token_quant else None
     with _device(dev):
-        _lib.call("qv_layernorm_quant", _ptr(x), dt, _ptr(_contig(weight)),
-                  _ptr(_contig(bias) if use_per_token_quant else None), _ptr(out), _ptr(scaling),
+        _lib.call("qv_layernorm_quant", _ptr(x), dt, _ptr(w), _ptr(b), _ptr(out), _ptr(scaling),
                   C.c_float(epsilon), 1 if use_per_token_quant else 0, M, D, _stream(dev))
 
 
@@ -435,9 +476,9 @@ def layernorm_forward_cuda(_input: torch.Tensor, _gamma: torch.Tensor, _out: tor
     if _gamma.numel() != D or _out.numel() != _input.numel():
         _fail(f"{what}: gamma must be ({D},) and out match input")
     dev = _on_gpu(_input, _gamma, _out, what=what)
+    x, g = _contig(_input), _contig(_gamma)
     with _device(dev):
-        _lib.call("qv_rmsnorm", _ptr(_contig(_input)), _ptr(_contig(_gamma)), _ptr(_out), C.c_float(eps),
-                  M, D, dt, _stream(dev))
+        _lib.call("qv_rmsnorm", _ptr(x), _ptr(g), _ptr(_out), C.c_float(eps), M, D, dt, _stream(dev))
 
 
 def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-6,
@@ -451,12 +492,14 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: f
     if weight.dtype != x.dtype or bias.dtype != x.dtype or weight.numel() != D or bias.numel() != D:
         _fail(f"{what}: weight/bias must be ({D},) {x.dtype}")
     dev = _on_gpu(x, weight, bias, out, what=what)
-    x = _contig(x)
+    x, w, b = _contig(x), _contig(weight), _contig(bias)
     if out is None:
         out = torch.empty_like(x)
+    elif out.dtype != x.dtype or out.numel() != x.numel() or not out.is_contiguous():
+        _fail(f"{what}: out must be a contiguous {x.dtype} tensor of {x.numel()} elements")
     with _device(dev):
-        _lib.call("qv_layernorm", _ptr(x), _ptr(_contig(weight)), _ptr(_contig(bias)), _ptr(out),
-                  C.c_float(eps), M, D, dt, _stream(dev))
+        _lib.call("qv_layernorm", _ptr(x), _ptr(w), _ptr(b), _ptr(out), C.c_float(eps), M, D, dt,
+                  _stream(dev))
     return out
 
 
@@ -483,9 +526,10 @@ def fused_rope_with_pos_forward_func(input: torch.Tensor, freqs: torch.Tensor,
         out = torch.empty(s, b, h, d, dtype=input.dtype, device=dev)
     xs = (C.c_int64 * 4)(*input.stride())
     os_ = (C.c_int64 * 4)(*out.stride())
+    fr = _contig(freqs)
     with _device(dev):
-        _lib.call("qv_rope_with_pos", _ptr(input), _ptr(_contig(freqs)), _ptr(out), dt, s, b, h, d, d2,
-                  xs, os_, _stream(dev))
+        _lib.call("qv_rope_with_pos", _ptr(input), _ptr(fr), _ptr(out), dt, s, b, h, d, d2, xs, os_,
+                  _stream(dev))
     return out
 
 
@@ -503,9 +547,7 @@ def rope2d(qkv: torch.Tensor, positions: torch.Tensor, cos_table: torch.Tensor, 
     T = qkv.numel() // qkv.shape[-1]
     if positions.dtype != torch.int32 or positions.numel() != 2 * T:
         _fail(f"{what}: positions must be int32 (T, 2)")
-    for t in (cos_table, sin_table):
-        if t.dtype != torch.float32 or t.shape[-1] != 16 or not t.is_contiguous():
-            _fail(f"{what}: tables must be contiguous float32 (P, 16)")
+    _check_rope_tables(cos_table, sin_table, what)
     dev = _on_gpu(qkv, positions, cos_table, sin_table, out, what=what)
     if not qkv.is_contiguous():
         _fail(f"{what}: qkv must be contiguous")
@@ -516,10 +558,10 @@ def rope2d(qkv: torch.Tensor, positions: torch.Tensor, cos_table: torch.Tensor, 
         dst_tok, dst_part = 3 * heads * 64, heads * 64
     else:
         dst_tok, dst_part = out.stride(0), heads * 64
+    pos = _contig(positions)
     with _device(dev):
-        _lib.call("qv_rope2d", _ptr(qkv), _ptr(out), _ptr(_contig(positions)), _ptr(cos_table),
-                  _ptr(sin_table), cos_table.shape[0], T, heads, 3 * heads * 64, dst_tok, dst_part,
-                  _stream(dev))
+        _lib.call("qv_rope2d", _ptr(qkv), _ptr(out), _ptr(pos), _ptr(cos_table), _ptr(sin_table),
+                  cos_table.shape[0], T, heads, 3 * heads * 64, dst_tok, dst_part, _stream(dev))
     return out
 
 
@@ -581,9 +623,12 @@ def qknorm_rope2d(qkv: torch.Tensor, positions: torch.Tensor, cos_table: torch.T
             _fail(f"{what}: {name} must be float16 (64,)")
     if positions.dtype != torch.int32 or positions.numel() != 2 * T:
         _fail(f"{what}: positions must be int32 (T, 2)")
+    _check_rope_tables(cos_table, sin_table, what)
     dev = _on_gpu(qkv, positions, cos_table, sin_table, q_gamma, q_beta, k_gamma, k_beta, what=what)
+    pos = _contig(positions)
+    qg, qb, kg, kb = _contig(q_gamma), _contig(q_beta), _contig(k_gamma), _contig(k_beta)
     with _device(dev):
-        _lib.call("qv_qknorm_rope2d", _ptr(qkv), _ptr(_contig(positions)), _ptr(cos_table), _ptr(sin_table),
-                  cos_table.shape[0], _ptr(_contig(q_gamma)), _ptr(_contig(q_beta)), _ptr(_contig(k_gamma)),
-                  _ptr(_contig(k_beta)), C.c_float(eps), T, heads, 3 * heads * 64, _stream(dev))
+        _lib.call("qv_qknorm_rope2d", _ptr(qkv), _ptr(pos), _ptr(cos_table), _ptr(sin_table),
+                  cos_table.shape[0], _ptr(qg), _ptr(qb), _ptr(kg), _ptr(kb), C.c_float(eps), T, heads,
+                  3 * heads * 64, _stream(dev))
     return qkv

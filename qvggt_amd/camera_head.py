@@ -20,8 +20,9 @@ head under the same module names:
 LayerNorm eps: 1e-5 (torch's default) for ``token_norm``, ``trunk_norm`` and
 the trunk blocks, 1e-6 for ``adaln_norm``.
 
-Per frame there is one pose token, so the trunk linears run at M = S: the
-W4A16 GEMV for S <= 16, the MFMA GEMM above.  Attention over S tokens with
+Per frame there is one pose token, so the trunk linears run at M = S: every
+S <= 64 runs on the skinny-M MFMA kernel (through the GEMV entry for
+S <= 16 and the GEMM entry above).  Attention over S tokens with
 head_dim 128 is a few kFLOP and runs in fp32 through torch.
 ``GraphedCameraHead`` records the whole forward as one HIP graph.  The CICT token
 QVGGT's loader can attach (loader.py:224-246) has no public definition and is

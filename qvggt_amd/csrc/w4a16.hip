@@ -1,231 +1,10 @@
-// AWQ W4A16 group-128 GEMM (small-tile path and dispatcher), skinny-M GEMV
-// and dequantisation for gfx950.  The AWQ-v2 nibble layout and the exact
-// dequantisation are documented in w4a16_common.h; the large-M streamed GEMM
-// lives in w4a16_stream.hip.
-//
-// MFMA mapping of the 128 x 128 kernel (v_mfma_f32_16x16x32_{f16,bf16}):
-// A operand = dequantised weights (row i = output channel n), B operand =
-// activations (column j = token m).  Lane (g = lane/16, l = lane%16) feeds 8
-// k-slots; for k-step t of a 128-k group the slot s of lane group g is
-// k = 32*g + 8*t + s on BOTH operands: activations are read as 8 contiguous
-// halves from LDS, weights are pair t of the lane's four words.  The output
-// lands as lane (g, l) holding out[m = l][n = 4*g + r], r = 0..3.
+// AWQ W4A16 group-128 dispatcher, skinny-M kernel (the GEMV entry and every
+// M <= 64), dequantisation and GPU packing for gfx950.  The AWQ-v2 nibble
+// layout and the exact dequantisation are documented in w4a16_common.h; the
+// large-M streamed GEMM lives in w4a16_stream.hip.
 #include "w4a16_common.h"
 
 namespace qv {
-
-// ------------------------------------------------------------ GEMM kernel
-// Workgroup: 256 threads = 4 waves arranged (BM/WM) x (BN/WN); tile BM x BN,
-// one 128-k group (= one scale row) per main-loop step.  Activations are
-// staged through double-buffered, padded LDS (register prefetch of the next
-// group overlaps the MFMAs of the current one); packed weights go straight
-// from global memory into registers and are dequantised there, so LDS traffic
-// is activations only.  Used for problems too small to fill the GPU with the
-// streamed kernel's 256-wide tiles.
-template <bool BF16, int BM, int BN, int WM, int WN, int EPI>
-__global__ __launch_bounds__(256) void w4a16_gemm_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K,
-    int tiles_n) {
-  constexpr int LDA = 128 + 8;  // halves per LDS row: 16-byte pad breaks bank aliasing
-  constexpr int RM = WM / 16;
-  constexpr int RN = WN / 16;
-  constexpr int WAVES_N = BN / WN;
-  static_assert((BM / WM) * (BN / WN) == 4, "4 waves per workgroup");
-  constexpr int A_CHUNKS = BM * 16 / 256;  // 16-byte chunks per thread per tile
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDA];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int g = lane >> 4, li = lane & 15;
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  const int m0 = (lid / tiles_n) * BM;
-  const int n0 = (lid % tiles_n) * BN;
-  const int wm0 = (wave / WAVES_N) * WM;
-  const int wn0 = (wave % WAVES_N) * WN;
-  const int KT = K >> 7;
-  const int K2 = K * 2;  // bytes per activation row = bytes per qweight row
-
-  // Buffer descriptors rebased on this tile: 32-bit offsets, and reads past
-  // the last valid row / channel return zeros (M and N tails need no clamps).
-  const auto rsA = make_rsrc(x + (size_t)m0 * K, (uint64_t)(M - m0) * K2);
-  const auto rsB = make_rsrc(qw + (size_t)(n0 >> 2) * (K >> 1), (uint64_t)((N - n0) >> 2) * K2);
-  const auto rsS = make_rsrc(scales + n0, ((uint64_t)KT * N - n0) * 2);
-  const auto rsZ = make_rsrc(zeros + n0, ((uint64_t)KT * N - n0) * 2);
-  // chunk c of the activation tile is row (tid>>4) + 16c, 16-byte column tid&15
-  const uint32_t a_voff = (uint32_t)((tid >> 4) * K2 + (tid & 15) * 16);
-  // subtile j is rows wn0 + 16j + li: qweight row ((wn0 + li) >> 2) + 4j
-  const int nl = wn0 + li;
-  const uint32_t b_voff =
-      (uint32_t)((nl >> 2) * K2 + ((g >> 1) * 32 + (li & 3) * 8 + (g & 1) * 4) * 4);
-  const uint32_t s_voff = (uint32_t)(nl * 2);
-
-  uint4 a_reg[A_CHUNKS];
-  uint4 b_reg[RN];
-  uint32_t s_reg[RN], z_reg[RN];
-
-  auto load_a = [&](int kt) {
-#pragma unroll
-    for (int c = 0; c < A_CHUNKS; ++c)
-      a_reg[c] = buf_load16(rsA, a_voff, c * 16 * K2 + kt * 256);
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int c = 0; c < A_CHUNKS; ++c) {
-      const int idx = tid + 256 * c;
-      *reinterpret_cast<uint4*>(&As[buf][(idx >> 4) * LDA + (idx & 15) * 8]) = a_reg[c];
-    }
-  };
-  auto load_b = [&](int kt) {
-#pragma unroll
-    for (int j = 0; j < RN; ++j) {
-      b_reg[j] = buf_load16(rsB, b_voff, j * 4 * K2 + kt * 256);
-      s_reg[j] = __builtin_amdgcn_raw_buffer_load_b16(rsS, s_voff, kt * N * 2 + j * 32, 0);
-      z_reg[j] = __builtin_amdgcn_raw_buffer_load_b16(rsZ, s_voff, kt * N * 2 + j * 32, 0);
-    }
-  };
-
-  f32x4 acc[RN][RM];
-#pragma unroll
-  for (int j = 0; j < RN; ++j)
-#pragma unroll
-    for (int i = 0; i < RM; ++i) acc[j][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  load_a(0);
-  load_b(0);
-  store_a(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < KT;
-    uint4 bq[RN];
-    uint32_t sq[RN], zq[RN];
-#pragma unroll
-    for (int j = 0; j < RN; ++j) {
-      bq[j] = b_reg[j];
-      sq[j] = s_reg[j];
-      zq[j] = z_reg[j];
-    }
-    if (more) {
-      load_a(kt + 1);
-      load_b(kt + 1);
-    }
-    const uint16_t* Ab = As[buf];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      uint4 bf[RM];
-#pragma unroll
-      for (int i = 0; i < RM; ++i)
-        bf[i] = *reinterpret_cast<const uint4*>(&Ab[(wm0 + 16 * i + li) * LDA + 32 * g + 8 * t]);
-#pragma unroll
-      for (int j = 0; j < RN; ++j) {
-        uint4 af;
-        switch (t) {
-          case 0: af = dq_frag<BF16, 0>(bq[j], sq[j], zq[j]); break;
-          case 1: af = dq_frag<BF16, 1>(bq[j], sq[j], zq[j]); break;
-          case 2: af = dq_frag<BF16, 2>(bq[j], sq[j], zq[j]); break;
-          default: af = dq_frag<BF16, 3>(bq[j], sq[j], zq[j]); break;
-        }
-#pragma unroll
-        for (int i = 0; i < RM; ++i) acc[j][i] = mfma16<BF16>(af, bf[i], acc[j][i]);
-      }
-    }
-    if (more) store_a(buf ^ 1);
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int j = 0; j < RN; ++j) {
-    const int n = n0 + wn0 + 16 * j + 4 * g;
-    if (n >= N) continue;
-#pragma unroll
-    for (int i = 0; i < RM; ++i) {
-      const int m = m0 + wm0 + 16 * i + li;
-      if (m < M) epilogue_store4<BF16, EPI>(out, bias, acc[j][i], m, n, N);
-    }
-  }
-}
-
-// ------------------------------------------------------------ GEMV kernel
-// One workgroup per 16 output channels; its W waves split the K groups
-// round-robin.  Lane (g, l) dequantises its 32 weights of row n0+l (chunk g)
-// and dots them with the matching 32 activations of every token with
-// v_dot2 (fp16 pairs, fp32 accumulate).  Partial sums are reduced across the
-// four lane groups with cross-lane shuffles and across waves through LDS.
-template <bool BF16, int MMAX>
-__global__ __launch_bounds__(1024) void w4a16_gemv_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int M, int N, int K, int epi) {
-  __shared__ float red[16][MMAX][16];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-  const int g = lane >> 4, li = lane & 15;
-  const int n = blockIdx.x * 16 + li;
-  const int KT = K >> 7;
-
-  float acc[MMAX];
-#pragma unroll
-  for (int m = 0; m < MMAX; ++m) acc[m] = 0.f;
-
-  for (int kt = wave; kt < KT; kt += nwaves) {
-    const uint4 wq = *reinterpret_cast<const uint4*>(qw + qw_chunk_u32(n, kt, g, K));
-    const uint32_t s = scales[(size_t)kt * N + n];
-    const uint32_t z = zeros[(size_t)kt * N + n];
-    uint4 wf[4];
-    wf[0] = dq_frag<BF16, 0>(wq, s, z);
-    wf[1] = dq_frag<BF16, 1>(wq, s, z);
-    wf[2] = dq_frag<BF16, 2>(wq, s, z);
-    wf[3] = dq_frag<BF16, 3>(wq, s, z);
-    const size_t kbase = (size_t)kt * 128 + 32 * g;
-#pragma unroll
-    for (int m = 0; m < MMAX; ++m) {
-      if (m < M) {
-        const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)m * K + kbase);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const uint4 xv = xp[t];
-          const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
-          const uint32_t ws[4] = {wf[t].x, wf[t].y, wf[t].z, wf[t].w};
-#pragma unroll
-          for (int f = 0; f < 4; ++f) {
-            if constexpr (BF16) {
-              acc[m] = __builtin_fmaf(__builtin_bit_cast(float, xs[f] << 16),
-                                      __builtin_bit_cast(float, ws[f] << 16), acc[m]);
-              acc[m] = __builtin_fmaf(__builtin_bit_cast(float, xs[f] & 0xFFFF0000u),
-                                      __builtin_bit_cast(float, ws[f] & 0xFFFF0000u), acc[m]);
-            } else {
-              acc[m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, xs[f]),
-                                              __builtin_bit_cast(f16x2, ws[f]), acc[m], false);
-            }
-          }
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int m = 0; m < MMAX; ++m) {
-    acc[m] += __shfl_xor(acc[m], 16);
-    acc[m] += __shfl_xor(acc[m], 32);
-  }
-  if (g == 0) {
-#pragma unroll
-    for (int m = 0; m < MMAX; ++m) red[wave][m][li] = acc[m];
-  }
-  __syncthreads();
-  for (int i = tid; i < M * 16; i += blockDim.x) {
-    const int m = i >> 4, l = i & 15;
-    float v = 0.f;
-    for (int w = 0; w < nwaves; ++w) v += red[w][m][l];
-    const int nn = blockIdx.x * 16 + l;
-    if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU) v += to_f32(bias[nn], BF16);
-    if (epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU) v = gelu_erf(v);
-    out[(size_t)m * N + nn] = from_f32<BF16>(v);
-  }
-}
 
 // ------------------------------------------------- skinny-M MFMA kernel
 // For M <= 64: one workgroup per 16 NB output channels whose W waves split
@@ -233,9 +12,11 @@ __global__ __launch_bounds__(1024) void w4a16_gemv_kernel(
 // but the products run on v_mfma_f32_16x16x32 with the dequantised weights
 // as the A operand (row = channel) and up to four 16-token column blocks of
 // activations as B, read with buffer loads straight from L2 (tokens >= M
-// fall outside the descriptor and read as zero).  Lane (g, l): channel
-// n0 + l, k-slots 32g + 8t .. +8 of step t, the slot map of the 128 x 128
-// kernel; accumulator block mb holds out[m = 16 mb + l][n = n0 + 4g + r].
+// fall outside the descriptor and read as zero).  Lane (g = lane/16,
+// l = lane%16): channel n0 + l; in k-step t of a 128-k group, k-slot s of the
+// lane is k = 32g + 8t + s on BOTH operands (activations: 8 contiguous
+// halves; weights: nibble pair t of the lane's four words of 32-k chunk g);
+// accumulator block mb holds out[m = 16 mb + l][n = n0 + 4g + r], r = 0..3.
 // Each weight byte is read once; the activations (M x K, at most 1 MiB at
 // K = 8192) stay L2-resident but are re-read by every workgroup, so NB > 1
 // (each activation fragment feeding NB channel blocks) cuts that L2 -> CU
@@ -474,71 +255,12 @@ __global__ __launch_bounds__(256) void w4a16_pack_tables_kernel(
 }
 
 // ------------------------------------------------------------- launchers
-template <bool BF16, int BM, int BN, int WM, int WN>
-static int launch_gemm_cfg(const void* x, const void* qw, const void* s, const void* z,
-                           const void* bias, void* out, int M, int N, int K, int epi,
-                           hipStream_t st) {
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  const dim3 grid(tiles_m * tiles_n), block(256);
-#define QV_GEMM_ARGS                                                                          \
-  (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,            \
-      (const uint16_t*)bias, (uint16_t*)out, M, N, K, tiles_n
-  switch (epi) {
-    case QV_EPI_NONE:
-      hipLaunchKernelGGL((w4a16_gemm_kernel<BF16, BM, BN, WM, WN, QV_EPI_NONE>), grid, block, 0, st, QV_GEMM_ARGS);
-      break;
-    case QV_EPI_BIAS:
-      hipLaunchKernelGGL((w4a16_gemm_kernel<BF16, BM, BN, WM, WN, QV_EPI_BIAS>), grid, block, 0, st, QV_GEMM_ARGS);
-      break;
-    case QV_EPI_BIAS_GELU:
-      hipLaunchKernelGGL((w4a16_gemm_kernel<BF16, BM, BN, WM, WN, QV_EPI_BIAS_GELU>), grid, block, 0, st, QV_GEMM_ARGS);
-      break;
-    default:
-      hipLaunchKernelGGL((w4a16_gemm_kernel<BF16, BM, BN, WM, WN, QV_EPI_GELU>), grid, block, 0, st, QV_GEMM_ARGS);
-      break;
-  }
-#undef QV_GEMM_ARGS
-  return check_launch("w4a16_gemm");
-}
-
 // Tile choice (w4_pick_tile): streamed kernel with BM = 128 / 96 / 64 / 32
 // (x 256); two workgroups run per CU (512 slots on 256 CUs).  M <= 64 goes to
 // the skinny kernel, whose grid covers the channels instead of M x N tiles.
-// The 128 x 128 register-staged kernel measured slower at every VGGT shape
-// and is kept for comparison runs.  QVGGT_W4_TILE=s128|s96|s64|s32|n128|skinny
-// forces one (tuning).
-static int w4_tile_override() {
-  static int v = [] {
-    const char* e = getenv("QVGGT_W4_TILE");
-    if (!e) return 0;
-    if (!strcmp(e, "s128")) return 1;
-    if (!strcmp(e, "s96")) return 2;
-    if (!strcmp(e, "s64")) return 3;
-    if (!strcmp(e, "n128")) return 4;
-    if (!strcmp(e, "skinny")) return 5;
-    if (!strcmp(e, "s32")) return 6;
-    return 0;
-  }();
-  return v;
-}
-
-// GEMV entry: the skinny MFMA kernel for every M (measured faster than the
-// v_dot2 GEMV from M = 1 on the VGGT shapes, where both are bound by load
-// latency, and up to 3.5x faster at M = 16, where the v_dot2 kernel is
-// VALU-bound).  QVGGT_W4_GEMV=dot keeps the v_dot2 kernel (comparison runs).
-static int w4_gemv_mfma_from() {
-  static int v = [] {
-    const char* e = getenv("QVGGT_W4_GEMV");
-    return (e && !strcmp(e, "dot")) ? 17 : 1;
-  }();
-  return v;
-}
-
 static int w4_pick_tile(int M, int N, int K) {
   // the skinny kernel addresses the activations with 32-bit buffer offsets
   const bool skinny_ok = M <= 64 && (int64_t)M * K * 2 < ((int64_t)1 << 31);
-  const int ov = w4_tile_override();
-  if (ov) return (ov == 5 && !skinny_ok) ? 1 : ov;
   if (skinny_ok) return 5;
   // Estimated time per candidate, in units of one 32-row tile step:
   //  * at most one tile per CU (256 tiles): latency-bound, a tile costs its
@@ -568,46 +290,20 @@ static int launch_skinny(const void* x, const void* qw, const void* s, const voi
 template <bool BF16>
 static int launch_gemm(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                        void* out, int M, int N, int K, int epi, hipStream_t st, const void* gamma = nullptr) {
-  int tile = w4_pick_tile(M, N, K);
-  if (tile == 4 && epi == QV_EPI_BIAS_RESID) tile = 1;  // the 128 x 128 kernel has no residual epilogue
-  switch (tile) {
-    case 1: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 128, st);
+  switch (w4_pick_tile(M, N, K)) {
     case 2: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 96, st);
     case 3: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 64, st);
     case 5: return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st, gamma);
     case 6: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 32, st);
-    default: return launch_gemm_cfg<BF16, 128, 128, 64, 64>(x, qw, s, z, bias, out, M, N, K, epi, st);
+    default: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 128, st);
   }
-}
-
-template <bool BF16>
-static int launch_gemv(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                       void* out, int M, int N, int K, int epi, hipStream_t st) {
-  const int KT = K / 128;
-  int waves = KT < 16 ? KT : 16;
-  const dim3 grid(N / 16), block(64 * waves);
-#define QV_GEMV(MM)                                                                            \
-  hipLaunchKernelGGL((w4a16_gemv_kernel<BF16, MM>), grid, block, 0, st, (const uint16_t*)x,    \
-                     (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,              \
-                     (const uint16_t*)bias, (uint16_t*)out, M, N, K, epi)
-  if (M <= 1) QV_GEMV(1);
-  else if (M <= 2) QV_GEMV(2);
-  else if (M <= 4) QV_GEMV(4);
-  else if (M <= 8) QV_GEMV(8);
-  else QV_GEMV(16);
-#undef QV_GEMV
-  return check_launch("w4a16_gemv");
 }
 
 // Channel blocks per skinny workgroup: NB = 2 from M = 5 when N >= 4096
 // (>= 128 workgroups remain), else 1 -- measured on the VGGT camera-head and
-// aggregator shapes, where NB = 4 never won (QVGGT_W4_SKINNY_NB=1|2 forces).
+// aggregator shapes, where NB = 4 never won.
 static int w4_skinny_nb(int M, int N) {
-  static int ov = [] {
-    const char* e = getenv("QVGGT_W4_SKINNY_NB");
-    return e ? atoi(e) : 0;
-  }();
-  int nb = (ov == 1 || ov == 2) ? ov : (M > 4 && N >= 4096) ? 2 : 1;
+  int nb = (M > 4 && N >= 4096) ? 2 : 1;
   if (N % (16 * nb)) nb = 1;
   return nb;
 }
@@ -647,7 +343,7 @@ static int check_common(const void* x, const void* qw, const void* s, const void
   QV_CHECK_ARG(M == 0 || (x && qw && s && z && out), "null pointer argument");
   QV_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)qw % 16) == 0, "x and qweight must be 16-byte aligned");
   QV_CHECK_ARG(((uintptr_t)s % 4) == 0 && ((uintptr_t)z % 4) == 0, "scale tables must be 4-byte aligned");
-  QV_CHECK_ARG(((uintptr_t)out % 8) == 0, "out must be 8-byte aligned");
+  QV_CHECK_ARG(((uintptr_t)out % 16) == 0, "out must be 16-byte aligned");
   QV_CHECK_ARG(bias == nullptr || ((uintptr_t)bias % 8) == 0, "bias must be 8-byte aligned");
   return QV_OK;
 }
@@ -678,15 +374,12 @@ extern "C" int qv_w4a16_gemv(const void* x, const void* qweight, const void* sca
   QV_CHECK_ARG(M >= 1 && M <= 16, "unsupported batch size M=%lld for the GEMV (1..16)", (long long)M);
   int rc = check_common(x, qweight, scales, scaled_zeros, bias, out, M, N, K, dtype, epilogue);
   if (rc) return rc;
+  // the skinny kernel addresses the activations with 32-bit buffer offsets
+  QV_CHECK_ARG(M * K * 2 < ((int64_t)1 << 31), "K=%lld too large for the GEMV", (long long)K);
   hipStream_t st = (hipStream_t)stream;
-  if (M >= w4_gemv_mfma_from() && M * K * 2 < ((int64_t)1 << 31)) {
-    if (dtype == QV_BF16)
-      return launch_skinny<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
-    return launch_skinny<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
-  }
   if (dtype == QV_BF16)
-    return launch_gemv<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
-  return launch_gemv<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+    return launch_skinny<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+  return launch_skinny<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
 }
 
 extern "C" int qv_w4a16_dequant(const void* qweight, const void* scales, const void* scaled_zeros,

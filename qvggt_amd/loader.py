@@ -11,6 +11,7 @@ as the checkpoint (``aggregator.frame_blocks.{i}.attn.qkv.qweight`` ...).
 * ``should_quantize_layer``          loader.py:320-362
 * ``quantize_specified_blocks``      loader.py:364-400 (nn.Linear -> WQLinear(init_only))
 * ``merge_state_dicts``              loader.py:466-548
+* ``load_model_config``              loader.py:146-162 (config.json, read as JSON)
 * ``load_quantized_aggregator``      loader.py:550-600 for the aggregator part
 * ``load_quantized_camera_head``     the same for ``camera_head.*`` (W4 trunk)
 
@@ -221,26 +222,52 @@ def _merged(quantized_path, model_path, quantize_type, frame_blocks, global_bloc
     return merged, cict, frame_blocks, global_blocks, layer_types, quantize_camera_head
 
 
+def load_model_config(quantized_path, model_path=None):
+    """The aggregator's model config (``AggregatorConfig``), found as the
+    reference finds its ``VGGTConfig`` (loader.py:146-162): the ``config.json``
+    in the directory of the original fp16 model when one is given; otherwise,
+    unlike the reference (which then takes the config class defaults), a
+    ``config.json`` beside the quantised checkpoint; otherwise the defaults.
+    The file is read as JSON only."""
+    from .aggregator import AggregatorConfig
+
+    for p in (model_path, quantized_path):
+        if p is None:
+            continue
+        d = Path(p)
+        if ((d if d.is_dir() else d.parent) / "config.json").exists():
+            return AggregatorConfig.from_pretrained(p)
+        if p is model_path:
+            break
+    return AggregatorConfig()
+
+
 @torch.no_grad()
-def load_quantized_aggregator(quantized_path, model_path=None, device="cuda", depth: int = 24,
+def load_quantized_aggregator(quantized_path, model_path=None, device="cuda", depth: int | None = None,
                               w_bit: int = 4, group_size: int = 128, quantize_type: str = "specific_blocks",
-                              frame_blocks=None, global_blocks=None, layer_types=None, strict: bool = True):
+                              frame_blocks=None, global_blocks=None, layer_types=None, strict: bool = True,
+                              config=None):
     """Build the aggregator for a QVGGT quantised checkpoint: fp16 model,
     selected linears swapped for ``WQLinear``, merged weights loaded.
 
-    For a self-contained checkpoint the layout (blocks, layer types) is
-    inferred from its ``.qweight`` keys, as loader.py:600-612 does.  Returns
-    (aggregator, report) with the replaced layer names and the checkpoint keys
-    the aggregator does not use (``strict`` raises on missing ones)."""
+    The model parameters (LayerNorm eps, depth, RoPE base) come from
+    ``config`` or, when that is None, from ``load_model_config``; ``depth``
+    overrides the config's depths.  For a self-contained checkpoint the layout
+    (blocks, layer types) is inferred from its ``.qweight`` keys, as
+    loader.py:600-612 does.  Returns (aggregator, report) with the replaced
+    layer names, the checkpoint keys the aggregator does not use (``strict``
+    raises on missing ones) and the config used."""
     from .aggregator import Aggregator
 
+    cfg = config if config is not None else load_model_config(quantized_path, model_path)
     merged, cict, frame_blocks, global_blocks, layer_types, _ = _merged(
         quantized_path, model_path, quantize_type, frame_blocks, global_blocks, layer_types, False)
-    agg = Aggregator.empty(device=device, depth=depth)
+    agg = Aggregator.empty(device=device, depth=depth, config=cfg)
     replaced = quantize_specified_blocks(agg, w_bit, group_size, quantize_type, frame_blocks, global_blocks,
                                          layer_types)
     missing, unused = _copy_into(agg, aggregator_state_dict(merged), strict, "aggregator")
-    return agg, {"replaced": replaced, "unused": unused, "missing": missing, "cict_token": cict}
+    return agg, {"replaced": replaced, "unused": unused, "missing": missing, "cict_token": cict,
+                 "config": agg.config}
 
 
 @torch.no_grad()

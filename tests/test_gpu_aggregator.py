@@ -147,3 +147,40 @@ def test_checkpoint_roundtrip_forward_is_identical(gpu, tmp_path):
     a, _ = src(img)
     c, _ = agg(img)
     assert torch.equal(a, c) and torch.isfinite(a.float()).all()
+
+
+def test_checkpoint_config_eps_reaches_the_kernels(gpu, tmp_path):
+    """A checkpoint whose config.json says LayerNorm eps 1e-5 (torch's default,
+    which VGGT's published blocks use) runs its AA blocks with eps 1e-5: on
+    low-variance rows (var ~ 1e-5, where eps matters) the loaded block matches
+    the oracle at eps 1e-5 and not at 1e-6 (loader.py:146-162 builds the model
+    from the checkpoint's config)."""
+    import json
+    from safetensors.torch import save_file
+    from qvggt_amd import aggregator as AG
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd import loader as LD
+    src = AG.Aggregator.random(w8a8=False, seed=13, device=gpu, depth=1, layerscale=1.0)
+    sd = {"aggregator." + k: v.detach().cpu().contiguous() for k, v in src.state_dict().items()
+          if not k.startswith("img_")}
+    sd["camera_head.pose_branch.fc1.weight"] = torch.zeros(4, 4, dtype=torch.float16)
+    save_file(sd, str(tmp_path / "model.safetensors"))
+    (tmp_path / "config.json").write_text(json.dumps({"layer_norm_eps": 1e-5, "depth": 1, "patch_embed_depth": 1}))
+    agg, rep = LD.load_quantized_aggregator(tmp_path / "model.safetensors", device=gpu)
+    blk = agg.frame_blocks[0]
+    assert rep["config"].block_ln_eps == 1e-5 and blk.eps == 1e-5
+    S = 1
+    M = S * AG.TOKENS
+    x0 = (np.random.default_rng(2).standard_normal((M, AG.DIM)) * 3e-3).astype(np.float16)
+    x = torch.from_numpy(x0).to(gpu)
+    pos = AG.vggt_positions(S, gpu)
+    blk(x, AG.TOKENS, pos, E.rope2d_tables(38, device=gpu), agg._workspace(M, gpu))
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(3).choice(M, 64, replace=False))
+    got = x.float().cpu().numpy()[rows] - x0.astype(np.float32)[rows]
+    c, s = R.rope2d_tables(38)
+    errs = {}
+    for eps in (1e-5, 1e-6):
+        ref = OA.aa_block_delta(x0, _params(blk), AG.TOKENS, pos.cpu().numpy(), c, s, rows, eps=eps)
+        errs[eps] = np.abs(got - ref).max() / np.abs(ref).max()
+    assert errs[1e-5] <= 1e-2 and errs[1e-6] > 5e-2, errs

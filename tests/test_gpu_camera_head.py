@@ -1,8 +1,9 @@
 """VGGT camera head with a W4A16 trunk on the GPU against the float64 oracle
 (oracle/camera_head.py).
 
-S pose tokens make the trunk linears run at M = S: S = 1 and 4 take the
-W4A16 GEMV, S = 24 the MFMA GEMM.  Every iteration's activated pose encoding
+S pose tokens make the trunk linears run at M = S: S = 1 and 4 go through
+the GEMV entry, S = 24 through the GEMM entry, and all three run on the
+skinny-M MFMA kernel.  Every iteration's activated pose encoding
 is compared; tolerance max|out - ref| / max|ref| <= 1e-2 (fp16 residual stream
 and activations vs the float64 reference with the same dequantised weights).
 """

@@ -266,3 +266,87 @@ def test_noncontiguous_activations_match_contiguous(gpu, M):
         want = E.gemm_forward_cuda_new(t["x"], t["qweight"], t["scales"], t["scaled_zeros"])
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+def test_bench_mlp_pair_instance(gpu):
+    """The exact launches bench.py times (config 2a, M = 8 x 1374): fc1
+    1024 -> 4096 with the bias + erf-GELU epilogue on the 128-row stream tile,
+    then fc2 4096 -> 1024 + bias from the GPU's own fc1 output, each against
+    the fp32 dequantised reference (+ float64 erf GELU)."""
+    from scipy.special import erf
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd._lib import QV_EPI_BIAS, QV_EPI_BIAS_GELU
+    M = 10992
+    p1 = O.make_w4_problem(M, 1024, 4096, seed=0)
+    p2 = O.make_w4_problem(M, 4096, 1024, seed=1)
+    b1 = (np.random.default_rng(5).standard_normal(4096) * 0.1).astype(np.float16)
+    b2 = (np.random.default_rng(6).standard_normal(1024) * 0.1).astype(np.float16)
+    t1, t2 = _to_dev(p1, gpu), _to_dev(p2, gpu)
+    h = E.w4a16_linear(t1["x"], t1["qweight"], t1["scales"], t1["scaled_zeros"], bias=torch.from_numpy(b1).to(gpu),
+                       epilogue=QV_EPI_BIAS_GELU)
+    y = E.w4a16_linear(h, t2["qweight"], t2["scales"], t2["scaled_zeros"], bias=torch.from_numpy(b2).to(gpu),
+                       epilogue=QV_EPI_BIAS)
+    torch.cuda.synchronize()
+    W1 = O.dequantize(p1["qweight"], p1["scales"], p1["scaled_zeros"], 4096, 1024)
+    pre = (O.gemm_ref(p1["x"], W1) + b1.astype(np.float32)).astype(np.float64)
+    ref1 = 0.5 * pre * (1.0 + erf(pre / np.sqrt(2.0)))
+    hn = h.float().cpu().numpy()
+    assert np.isfinite(hn).all() and O.rel_err(hn, ref1) <= TOL
+    W2 = O.dequantize(p2["qweight"], p2["scales"], p2["scaled_zeros"], 1024, 4096)
+    ref2 = O.gemm_ref(h.cpu().numpy(), W2) + b2.astype(np.float32)
+    assert O.rel_err(y.float().cpu().numpy(), ref2) <= TOL
+
+
+def test_noncontiguous_tables_match_contiguous(gpu):
+    """Transposed-view scales, zeros, bias (and LayerNorm / qk-norm weights)
+    give the same bits as their contiguous copies: each strided argument is
+    copied to a buffer that stays alive until the kernel has been launched."""
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd._lib import QV_EPI_BIAS
+    M, N, K = 300, 1024, 1024
+    p = O.make_w4_problem(M, K, N, seed=31)
+    t = _to_dev(p, gpu)
+    sT = t["scales"].t().contiguous().t()        # same shape, column-major
+    zT = t["scaled_zeros"].t().contiguous().t()
+    assert not sT.is_contiguous() and not zT.is_contiguous()
+    bias = torch.linspace(-1, 1, 2 * N, device=gpu).half()[::2]
+    for m in (M, 5):
+        want = E.w4a16_linear(t["x"][:m], t["qweight"], t["scales"], t["scaled_zeros"], bias=bias.contiguous(),
+                              epilogue=QV_EPI_BIAS)
+        got = E.w4a16_linear(t["x"][:m], t["qweight"], sT, zT, bias=bias, epilogue=QV_EPI_BIAS)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+    xg = torch.randn(64, 1024, generator=torch.Generator().manual_seed(0)).half().to(gpu)
+    w = torch.linspace(0.5, 1.5, 2048, device=gpu).half()[::2]
+    b = torch.linspace(-0.5, 0.5, 2048, device=gpu).half()[1::2]
+    assert torch.equal(E.layer_norm(xg, w, b), E.layer_norm(xg, w.contiguous(), b.contiguous()))
+    q1, q2 = (torch.empty(64, 1024, dtype=torch.int8, device=gpu) for _ in range(2))
+    s1, s2 = (torch.empty(64, dtype=torch.float16, device=gpu) for _ in range(2))
+    E.rms_norm_general(q1, xg, w, b, s1, 1e-6, True)
+    E.rms_norm_general(q2, xg, w.contiguous(), b.contiguous(), s2, 1e-6, True)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+
+
+def test_output_must_be_16_byte_aligned(gpu):
+    """The stream GEMM's epilogue stores 16-byte row pieces: an output view
+    offset by 8 bytes is refused with a clear error (by the Python op and by
+    the C ABI itself), never written misaligned."""
+    import ctypes as C
+    from qvggt_amd import _lib
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd._lib import QV_EPI_NONE, QV_F16
+    M, N, K = 300, 1024, 1024
+    p = O.make_w4_problem(M, K, N, seed=41)
+    t = _to_dev(p, gpu)
+    buf = torch.zeros(M * N + 4, dtype=torch.float16, device=gpu)
+    bad = buf[4:].view(M, N)
+    assert bad.data_ptr() % 16 == 8
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], out=bad)
+    ptr = lambda v: C.c_void_p(v.data_ptr())
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        _lib.call("qv_w4a16_gemm", ptr(t["x"]), ptr(t["qweight"]), ptr(t["scales"]), ptr(t["scaled_zeros"]),
+                  C.c_void_p(0), ptr(bad), M, N, K, QV_F16, QV_EPI_NONE, C.c_void_p(0))
+    torch.cuda.synchronize()
+    assert not buf.any()

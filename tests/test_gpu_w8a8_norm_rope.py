@@ -27,14 +27,33 @@ def _rng(seed):
     return np.random.default_rng(seed)
 
 
+_TORCH_DT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def _as(x, dt: str) -> np.ndarray:
+    """fp32 values of storage type ``dt`` (exactly representable in it)."""
+    return Q.round_store(np.asarray(x, np.float32), dt)
+
+
+def _dev(x32: np.ndarray, dt: str, gpu) -> torch.Tensor:
+    """A device tensor of type ``dt`` holding the fp32 values x32 exactly."""
+    return torch.from_numpy(np.ascontiguousarray(x32, np.float32)).to(_TORCH_DT[dt]).to(gpu)
+
+
+def _vals(t: torch.Tensor) -> np.ndarray:
+    """fp32 values of a device tensor (exact for fp16 / bf16 / fp32)."""
+    return t.detach().float().cpu().numpy()
+
+
 # ----------------------------------------------------------- quantisation
-@pytest.mark.parametrize("M,D,dt", [(1374, 1024, np.float16), (10992, 1024, np.float16), (300, 4096, np.float32),
-                                    (5, 8, np.float16), (64, 8192, np.float16)])
+@pytest.mark.parametrize("M,D,dt", [(1374, 1024, "f16"), (10992, 1024, "f16"), (300, 4096, "f32"),
+                                    (5, 8, "f16"), (64, 8192, "f16"), (777, 1024, "bf16"), (3, 4096, "bf16")])
 def test_invoke_quant_bit_exact(gpu, M, D, dt):
+    """quantization.cu:87-95 dispatches float, half and bfloat16."""
     from qvggt_amd import awq_inference_engine as E
-    x = (_rng(M + D).standard_normal((M, D)) * 3).astype(dt)
+    x = _as(_rng(M + D).standard_normal((M, D)) * 3, dt)
     x[0] = 0  # amax = 0 row
-    xt = torch.from_numpy(x).to(gpu)
+    xt = _dev(x, dt, gpu)
     q = torch.empty(M, D, dtype=torch.int8, device=gpu)
     s = torch.empty(M, dtype=torch.float16, device=gpu)
     E.invoke_quant(q, xt, s)
@@ -76,33 +95,64 @@ def test_w8a8_gemm_fp16_bit_exact(gpu, M, N, K, bias):
 
 
 # ------------------------------------------------------- LN + quant
-@pytest.mark.parametrize("M,D", [(10992, 1024), (33, 4096), (7, 1000)])
-def test_rms_norm_general_per_token_bit_exact(gpu, M, D):
+@pytest.mark.parametrize("M,D,dt", [(10992, 1024, "f16"), (33, 4096, "f16"), (7, 1000, "f16"),
+                                    (1374, 1024, "bf16"), (65, 4096, "bf16"), (300, 1024, "f32"), (9, 2048, "f32")])
+def test_rms_norm_general_per_token_bit_exact(gpu, M, D, dt):
+    """layernorm.cu:166-190 dispatches float, half and bfloat16."""
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(M + D)
-    x = (rng.standard_normal((M, D)) * 2 + 0.5).astype(np.float16)
-    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float16)
-    b = (0.1 * rng.standard_normal(D)).astype(np.float16)
+    x = _as(rng.standard_normal((M, D)) * 2 + 0.5, dt)
+    g = _as(1 + 0.1 * rng.standard_normal(D), dt)
+    b = _as(0.1 * rng.standard_normal(D), dt)
     q = torch.empty(M, D, dtype=torch.int8, device=gpu)
     s = torch.empty(M, dtype=torch.float16, device=gpu)
-    E.rms_norm_general(q, torch.from_numpy(x).to(gpu), torch.from_numpy(g).to(gpu), torch.from_numpy(b).to(gpu),
-                       s, 1e-6, True)
-    qr, sr = Q.layernorm_quant(x, g, b, 1e-6)
+    E.rms_norm_general(q, _dev(x, dt, gpu), _dev(g, dt, gpu), _dev(b, dt, gpu), s, 1e-6, True)
+    qr, sr = Q.layernorm_quant(x, g, b, 1e-6, dt)
     assert np.array_equal(q.cpu().numpy(), qr)
     assert np.array_equal(_bits(s), sr.view(np.int16))
 
 
-def test_rms_norm_general_per_tensor_bit_exact(gpu):
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+def test_rms_norm_general_per_tensor_bit_exact(gpu, dt):
+    """Per-tensor scale (layernorm.cu:100-123): a nonzero beta is passed and
+    must be ignored (the host passes nullptr, layernorm.cu:180-187).  Random
+    rows against the oracle; rows with a closed-form LayerNorm (eps = 0,
+    [4, -4, ...] -> +-gamma and [2, -2, 0, 0, ...] -> +-sqrt 2 rounded to the
+    storage type) against their known codes."""
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(9)
     M, D = 500, 1024
-    x = rng.standard_normal((M, D)).astype(np.float16)
-    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float16)
+    x = _as(rng.standard_normal((M, D)), dt)
+    g = _as(1 + 0.1 * rng.standard_normal(D), dt)
+    beta = _dev(_as(0.5 + rng.standard_normal(D), dt), dt, gpu)
     sc = np.array([24.0], np.float16)
     q = torch.empty(M, D, dtype=torch.int8, device=gpu)
-    E.rms_norm_general(q, torch.from_numpy(x).to(gpu), torch.from_numpy(g).to(gpu), None,
-                       torch.from_numpy(sc).to(gpu), 1e-6, False)
-    assert np.array_equal(q.cpu().numpy(), Q.layernorm_quant_per_tensor(x, g, 1e-6, sc[0]))
+    E.rms_norm_general(q, _dev(x, dt, gpu), _dev(g, dt, gpu), beta, torch.from_numpy(sc).to(gpu), 1e-6, False)
+    assert np.array_equal(q.cpu().numpy(), Q.layernorm_quant_per_tensor(x, g, 1e-6, sc[0], dt))
+    # closed-form rows
+    xk = np.stack([np.tile(np.array([4.0, -4.0], np.float32), D // 2),
+                   np.tile(np.array([2.0, -2.0, 0.0, 0.0], np.float32), D // 4)])
+    gk = _as(np.linspace(-40, 40, D), dt)
+    gk[0::4] = 1.0        # columns 0 and 1 of the sqrt-2 row see gamma 1
+    gk[1::4] = 1.0
+    # an fp16 scale at which rint(T(sqrt 2) * s) != rint(sqrt(2) * s) for T = fp16 / bf16
+    cand = np.unique(np.arange(1.0, 89.0, 2 ** -8).astype(np.float16)).astype(np.float64)
+    sck = np.array([cand[np.rint(1.4140625 * cand) != np.rint(np.sqrt(2.0) * cand)][0]], np.float16)
+    qk = torch.empty(2, D, dtype=torch.int8, device=gpu)
+    E.rms_norm_general(qk, _dev(xk, dt, gpu), _dev(gk, dt, gpu), beta, torch.from_numpy(sck).to(gpu), 0.0, False)
+    got = qk.cpu().numpy()
+    sign = np.where(np.arange(D) % 2 == 0, 1.0, -1.0)
+    want0 = np.clip(np.rint(sign * gk.astype(np.float64) * float(sck[0])), -128, 127)
+    assert np.array_equal(got[0], want0.astype(np.int8))
+    s32 = np.float32(sck[0])
+    if dt == "f32":   # fp32 keeps LN = 2 * fp32(1/fp32(sqrt 2)); the product rounds in fp32
+        ln = np.float32(2.0) * (np.float32(1.0) / np.sqrt(np.float32(2.0)))
+        want = np.rint(np.float32(ln * s32))
+    else:             # fp16 and bf16 both round sqrt 2 to 1.4140625
+        want = np.rint(1.4140625 * float(s32))
+        assert want != np.rint(np.sqrt(2.0) * float(s32))
+    assert got[1, 0] == want and got[1, 1] == -want and got[1, 2] == 0 and got[1, 3] == 0
+    assert np.array_equal(got, Q.layernorm_quant_per_tensor(xk, gk, 0.0, sck[0], dt))
 
 
 @pytest.mark.parametrize("M,D", [(2748, 4096), (3, 64)])
@@ -182,16 +232,26 @@ def test_gelu_non_finite_inputs_match_oracle(gpu):
 
 
 # ------------------------------------------------------- normalisation
-@pytest.mark.parametrize("shape", [(4, 300, 1024), (2, 7, 4096), (1, 1, 64)])
-def test_layernorm_forward_cuda_rmsnorm_bit_exact(gpu, shape):
+@pytest.mark.parametrize("shape,dt", [((4, 300, 1024), "f16"), ((2, 7, 4096), "f16"), ((1, 1, 64), "f16"),
+                                      ((3, 333, 1024), "bf16"), ((1, 5, 4096), "bf16")])
+def test_layernorm_forward_cuda_rmsnorm_bit_exact(gpu, shape, dt):
+    """layernorm/layernorm.cu:8-19 dispatches half and bfloat16 (the half
+    output is clamped, the bfloat16 one is not)."""
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(sum(shape))
-    x = rng.standard_normal(shape).astype(np.float16)
-    g = rng.uniform(0.5, 1.5, shape[-1]).astype(np.float16)
-    out = torch.empty(shape, dtype=torch.float16, device=gpu)
-    E.layernorm_forward_cuda(torch.from_numpy(x).to(gpu), torch.from_numpy(g).to(gpu), out, 1e-6)
-    ref = Q.rmsnorm(x.reshape(-1, shape[-1]), g, 1e-6).reshape(shape)
-    assert np.array_equal(_bits(out), ref.view(np.int16))
+    x = _as(rng.standard_normal(shape) * (1 if dt == "f16" else 3), dt)
+    g = _as(rng.uniform(0.5, 1.5, shape[-1]), dt)
+    if dt == "bf16":
+        g[:4] = 1e5 * np.array([1, -1, 3, -3], np.float32)   # beyond the fp16 range: no clamp for bf16
+        g = _as(g, dt)
+    out = torch.empty(shape, dtype=_TORCH_DT[dt], device=gpu)
+    E.layernorm_forward_cuda(_dev(x, dt, gpu), _dev(g, dt, gpu), out, 1e-6)
+    ref = Q.rmsnorm(x.reshape(-1, shape[-1]), g, 1e-6, dt).reshape(shape)
+    if dt == "f16":
+        assert np.array_equal(_bits(out), ref.view(np.int16))
+    else:
+        assert np.array_equal(_vals(out).view(np.int32), ref.astype(np.float32).view(np.int32))
+        assert np.abs(_vals(out)).max() > 65504
 
 
 @pytest.mark.parametrize("M", [10992, 1374, 1])
@@ -208,8 +268,11 @@ def test_vggt_layer_norm_bit_exact(gpu, M):
 
 # ------------------------------------------------------------------ RoPE
 @pytest.mark.parametrize("transpose_out", [False, True])
-@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32, torch.bfloat16])
 def test_fused_rope_with_pos(gpu, transpose_out, dt):
+    """fused_rope_with_pos.cu:155-161 dispatches float, half and bfloat16.
+    fp16 / bf16 within one ulp of the oracle's rounding (and equal in more
+    than 99.9 % of elements), fp32 within 2e-6 relative."""
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(3)
     S, B, H, D, D2 = 37, 3, 16, 64, 48
@@ -217,14 +280,22 @@ def test_fused_rope_with_pos(gpu, transpose_out, dt):
     freqs = rng.uniform(-20, 20, (B, S, D2)).astype(np.float32)
     xt = torch.from_numpy(base).to(gpu).to(dt).transpose(0, 1)   # (S,B,H,D), non-contiguous
     y = E.fused_rope_with_pos_forward_func(xt, torch.from_numpy(freqs).to(gpu), transpose_out)
-    assert y.shape == (S, B, H, D)
-    ref = R.rope_with_pos(xt.cpu().numpy(), freqs)
-    got = y.cpu().numpy()
-    if dt == torch.float16:
+    assert y.shape == (S, B, H, D) and y.dtype == dt
+    if dt == torch.bfloat16:
+        ref = R.rope_with_pos(_vals(xt), freqs, "bf16")
+        got = _vals(y)
+        ulp = np.abs(ref) * 2.0 ** -7          # one bf16 ulp is at most 2**-7 of the value
+        assert (np.abs(got - ref) <= np.maximum(ulp, 1e-30)).all()
+        assert (got == ref).mean() > 0.999
+    elif dt == torch.float16:
+        ref = R.rope_with_pos(xt.cpu().numpy(), freqs)
+        got = y.cpu().numpy()
         ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
         assert (np.abs(got.astype(np.float32) - ref.astype(np.float32)) <= ulp).all()
         assert (got == ref).mean() > 0.999
     else:
+        ref = R.rope_with_pos(xt.cpu().numpy(), freqs)
+        got = y.cpu().numpy()
         assert np.abs(got - ref).max() <= 2e-6 * max(1.0, np.abs(ref).max())
 
 

@@ -59,6 +59,35 @@ def test_gemv_errors_match_reference_messages():
         E.gemv_forward_cuda_new(x[:2], qw, sc, sc, 2, 64, 256, 64)
 
 
+def test_host_checks_reject_bad_shapes_before_any_launch():
+    """Shapes that would make a kernel read or write out of bounds are refused
+    on the host: an activation whose last dim is not k (the GEMV sizes its
+    output from it), a caller-provided GEMM output of the wrong shape, dtype,
+    layout or alignment, and RoPE tables narrower than (P, 16)."""
+    m, n, k = 2, 64, 256
+    qw = torch.zeros(n // 4, k, dtype=torch.int16)
+    sc = torch.zeros(8, n, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="in_feats must be"):
+        E.gemv_forward_cuda_new(torch.zeros(1, m * k, dtype=torch.float16), qw, sc, sc, m, n, k, 128)
+    x = torch.zeros(m, k, dtype=torch.float16)
+    for bad, msg in ((torch.zeros(m, n + 16, dtype=torch.float16), "out must be a contiguous"),
+                     (torch.zeros(m, n, dtype=torch.float32), "out must be a torch.float16"),
+                     (torch.zeros(n, m, dtype=torch.float16).t(), "out must be a contiguous"),
+                     (torch.zeros(m * n + 4, dtype=torch.float16)[4:].view(m, n), "16-byte aligned")):
+        with pytest.raises(RuntimeError, match=msg):
+            E.w4a16_linear(x, qw, sc, sc, out=bad)
+    T, H = 5, 16
+    qkv = torch.zeros(T, 3 * H * 64, dtype=torch.float16)
+    pos = torch.zeros(T, 2, dtype=torch.int32)
+    g = torch.ones(64, dtype=torch.float16)
+    for c, s_ in ((torch.zeros(38, 8), torch.zeros(38, 8)), (torch.zeros(38, 16, dtype=torch.float64),) * 2,
+                  (torch.zeros(38, 16), torch.zeros(30, 16)), (torch.zeros(16, 38).t(), torch.zeros(38, 16))):
+        with pytest.raises(RuntimeError, match="tables|differ"):
+            E.qknorm_rope2d(qkv, pos, c, s_, H, g, g, g, g)
+        with pytest.raises(RuntimeError, match="tables|differ"):
+            E.rope2d(qkv, pos, c, s_, H)
+
+
 def test_ops_refuse_cpu_tensors_and_bad_dtypes():
     x = torch.zeros(16, 256, dtype=torch.float16)
     qw = torch.zeros(16, 256, dtype=torch.int16)

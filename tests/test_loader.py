@@ -124,3 +124,33 @@ def test_roundtrip_quantized_camera_head_checkpoint(tmp_path):
     assert got.keys() == ref.keys()
     for k in ref:
         assert got[k].dtype == ref[k].dtype and torch.equal(got[k], ref[k]), k
+
+
+def test_model_config_is_read_like_the_reference(tmp_path):
+    """The aggregator's eps / depth come from the checkpoint's config.json
+    (loader.py:146-162 reads VGGTConfig from the fp16 model's directory): a
+    config with LayerNorm eps 1e-5 and depth 2 builds blocks whose four norms
+    use 1e-5; the fp16 model's directory wins over the checkpoint's; no
+    config gives the defaults; unsupported dims are refused."""
+    import json
+    from safetensors.torch import save_file
+    from qvggt_amd.aggregator import AggregatorConfig
+    src = Aggregator.random(w8a8=False, seed=1, device="cpu", depth=2)
+    sd = {"aggregator." + k: v.contiguous() for k, v in src.state_dict().items() if not k.startswith("img_")}
+    sd["camera_head.pose_branch.fc1.weight"] = torch.zeros(4, 4, dtype=torch.float16)
+    qdir, mdir = tmp_path / "q", tmp_path / "m"
+    qdir.mkdir()
+    mdir.mkdir()
+    save_file(sd, str(qdir / "model.safetensors"))
+    assert LD.load_model_config(qdir / "model.safetensors") == AggregatorConfig()
+    (qdir / "config.json").write_text(json.dumps({"layer_norm_eps": 1e-5, "depth": 2, "patch_embed_depth": 2,
+                                                  "rope_freq": 100}))
+    agg, rep = LD.load_quantized_aggregator(qdir / "model.safetensors", device="cpu")
+    assert rep["config"].block_ln_eps == 1e-5 and rep["config"].depth == 2 and len(agg.frame_blocks) == 2
+    for blk in list(agg.frame_blocks) + list(agg.global_blocks):
+        assert blk.eps == 1e-5
+        assert {m.eps for m in (blk.norm1, blk.norm2, blk.attn.q_norm, blk.attn.k_norm)} == {1e-5}
+    (mdir / "config.json").write_text(json.dumps({"aggregator": {"layer_norm_eps": 3e-6, "depth": 2}}))
+    assert LD.load_model_config(qdir / "model.safetensors", mdir / "w.pt").block_ln_eps == 3e-6
+    with pytest.raises(ValueError, match="unsupported"):
+        AggregatorConfig.from_dict({"hidden_size": 768})

@@ -109,6 +109,86 @@ def test_rmsnorm_matches_float64_and_clamps():
     assert np.isfinite(big.astype(np.float32)).all()
 
 
+def _sqrt2_scales():
+    """fp16 scales s in [1, 89] for which rint(fp16(sqrt 2) * s) differs from
+    rint(sqrt(2) * s): the int8 code then tells whether the LayerNorm value was
+    rounded to fp16 before the multiply."""
+    r16 = 1.4140625                       # fp16(sqrt 2): 1448 * 2**-10
+    cands = np.arange(1.0, 89.0, 2 ** -8).astype(np.float16)
+    cands = np.unique(cands).astype(np.float64)
+    hit = cands[np.rint(r16 * cands) != np.rint(math.sqrt(2.0) * cands)]
+    assert hit.size >= 3
+    return hit
+
+
+def test_layernorm_quant_per_tensor_known_answers():
+    """rms_norm_general with a per-tensor scale (w8a8/layernorm.cu:100-123;
+    the host passes beta = nullptr, layernorm.cu:180-187):
+    q = sat(rint(float(fp16(LN(x) * gamma)) * scale)), no beta, no amax.
+
+    Rows with a closed-form LayerNorm (eps = 0):
+    * [4, -4, 4, -4, ...]: mean 0, variance 16, LN = +-1 exactly, so
+      q = sat(rint(+-gamma * scale)) -- gamma is applied, the scale multiplies
+      (dividing would give rint(gamma / scale)), ties go to even and codes
+      saturate at 127 / -128;
+    * [2, -2, 0, 0, ...]: LN = +-sqrt(2), 0; fp16 rounds sqrt 2 to 1.4140625,
+      and at the scales of ``_sqrt2_scales`` only the fp16-rounded value gives
+      the oracle's code."""
+    D = 1024
+    x1 = np.tile(np.array([4.0, -4.0], np.float32), D // 2)[None]
+    gam = np.float16(np.linspace(-40, 40, D)).astype(np.float32)
+    for sc in (4.5, 0.25, 3.0):
+        q = Q.layernorm_quant_per_tensor(x1, gam, 0.0, np.float16(sc))[0]
+        sign = np.where(np.arange(D) % 2 == 0, 1.0, -1.0)
+        want = np.clip(np.rint(sign * gam.astype(np.float64) * sc), -128, 127)
+        assert np.array_equal(q, want.astype(np.int8)), sc
+    # a tie: gamma 3 * scale 4.5 = 13.5 -> 14 (even), 2.5 * 1 = 2.5 -> 2
+    g2 = np.full(D, 3.0, np.float32)
+    g2[1::2] = 2.5
+    q = Q.layernorm_quant_per_tensor(x1, g2, 0.0, np.float16(4.5))[0]
+    assert q[0] == 14 and q[2] == 14 and q[1] == -11   # -2.5 * 4.5 = -11.25 -> -11
+    q = Q.layernorm_quant_per_tensor(x1, g2, 0.0, np.float16(1.0))[0]
+    assert q[0] == 3 and q[1] == -2                      # -2.5 -> -2 (even)
+    x2 = np.tile(np.array([2.0, -2.0, 0.0, 0.0], np.float32), D // 4)[None]
+    ones = np.ones(D, np.float32)
+    for sc in _sqrt2_scales()[:8]:
+        q = Q.layernorm_quant_per_tensor(x2, ones, 0.0, np.float16(sc))[0]
+        assert q[0] == np.rint(1.4140625 * sc) != np.rint(math.sqrt(2.0) * sc), sc
+        assert q[1] == -q[0] and q[2] == 0 and q[3] == 0
+
+
+def test_layernorm_quant_storage_types():
+    """bf16 / fp32 inputs (layernorm.cu dispatches half, bfloat16, float): the
+    LayerNorm value is rounded to the input type before the per-tensor int8
+    conversion and before the per-token amax, whose floor is T(1e-6)."""
+    D = 1024
+    x2 = np.tile(np.array([2.0, -2.0, 0.0, 0.0], np.float32), D // 4)[None]
+    ones = np.ones(D, np.float32)
+    # bf16(sqrt 2) = 1.4140625 as well (8 significant bits: 181 * 2**-7); fp32 keeps sqrt 2
+    sc = float(_sqrt2_scales()[0])
+    assert Q.layernorm_quant_per_tensor(x2, ones, 0.0, sc, "bf16")[0, 0] == np.rint(1.4140625 * sc)
+    assert Q.layernorm_quant_per_tensor(x2, ones, 0.0, sc, "f32")[0, 0] == np.rint(
+        np.float32(np.float32(2.0) * np.float32(1.0) / np.sqrt(np.float32(2.0))) * np.float32(sc))
+    # per-token floor: an all-equal row has LN = 0 everywhere, so amax = T(1e-6);
+    # fp32 1e-6 is 0x358637BD, which bf16 truncates (low half < 0x8000) to 0x35860000
+    assert np.float32(1e-6).view(np.uint32) == 0x358637BD
+    flat = np.full((1, 64), 3.0, np.float32)
+    for dt, floor in (("f16", np.float32(np.float16(1e-6))), ("f32", np.float32(1e-6)),
+                      ("bf16", np.uint32(0x35860000).view(np.float32))):
+        q, s = Q.layernorm_quant(flat, np.ones(64, np.float32), np.zeros(64, np.float32), 1e-6, dt)
+        assert not q.any() and s[0] == np.float16(floor / np.float32(127.0)), dt
+
+
+def test_round_store_known_answers():
+    v = np.array([1.0, 1.00390625, 1.005859375, 1.0029296875, -3.0, 65520.0, 1e-6], np.float32)
+    # bf16 keeps 8 significant bits: ties to even at 1 + 2**-8, 1 + 3*2**-9 rounds up
+    assert Q.round_store(v[:5], "bf16").tolist() == [1.0, 1.0, 1.0078125, 1.0, -3.0]
+    assert Q.round_store(v, "f16").tolist()[:5] == [1.0, 1.00390625, 1.005859375, 1.0029296875, -3.0]
+    with np.errstate(over="ignore"):
+        assert np.isinf(Q.round_store(v[5:6], "f16")[0])   # past the fp16 range
+    assert Q.round_store(v, "f32").tolist() == v.tolist()
+
+
 # ------------------------------------------------------------- GELU
 def test_gelu_fast_close_to_closed_form():
     x = np.linspace(-6, 6, 4097).astype(np.float16)
