@@ -142,7 +142,9 @@ def aggregator_fps(dev, S: int = 32, reps: int = 3, w8a8: bool = False):
 
 
 def _time_graph(fn, calls: int, reps: int = 3):
-    """Capture `calls` invocations of fn(i) in one HIP graph, replay, return us per call."""
+    """Capture `calls` invocations of fn(i) in one HIP graph, replay, return us per call.
+    The graph is captured on the stream that ran the warm-up calls, so the ops'
+    per-stream split-K workspaces already exist when capture starts."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -152,7 +154,7 @@ def _time_graph(fn, calls: int, reps: int = 3):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for i in range(calls):
             fn(i)
     g.replay()

@@ -188,7 +188,9 @@ class GraphedCameraHead:
                 head(self.tokens, num_iterations)
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        # captured on the warmed-up stream: the W4 ops' per-stream split-K
+        # workspaces exist by now (none may be allocated during capture)
+        with torch.cuda.graph(self.graph, stream=side):
             self.outs = head(self.tokens, num_iterations)
 
     @torch.no_grad()

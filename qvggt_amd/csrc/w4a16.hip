@@ -4,6 +4,10 @@
 // large-M streamed GEMM lives in w4a16_stream.hip.
 #include "w4a16_common.h"
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 namespace qv {
 
 // ------------------------------------------------- skinny-M MFMA kernel
@@ -22,20 +26,32 @@ namespace qv {
 // (each activation fragment feeding NB channel blocks) cuts that L2 -> CU
 // traffic by NB at the cost of NB-fold fewer workgroups.  Wave partials are
 // summed through LDS.
+//
+// Split K (gridDim.y = SK > 1): workgroup (b, ks) takes the 128-k groups
+// [ks*KT/SK, (ks+1)*KT/SK) of channel block b, so a launch with few channel
+// blocks (e.g. 8192 -> 2048: 128 blocks) still fills the CUs.  Each split
+// writes its fp32 partial (M x 16 NB) to workspace slot (b, ks) with
+// agent-coherent (sc1) stores, waits for them (vmcnt 0) and bumps block b's
+// arrival counter; the split that arrives last reads the SK partials back in
+// ks order -- the sum order never depends on arrival order -- runs the
+// epilogue and resets the counter to zero for the next launch.  No workgroup
+// waits on another.
 template <bool BF16, int MB, int NB>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB == 1 ? 8 : 1))) void w4a16_skinny_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out,
-    int M, int N, int K, int epi) {
+    int M, int N, int K, int epi, float* __restrict__ part, int* __restrict__ cnt) {
   __shared__ f32x4 red[16][MB][64];
+  __shared__ int s_arrived;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nwaves = blockDim.x >> 6;
   const int g = lane >> 4, li = lane & 15;
   const int n0 = blockIdx.x * 16 * NB;
-  const int KT = K >> 7;
+  const int SK = gridDim.y, ks = blockIdx.y;
+  const int kt_lo = (int)((int64_t)ks * (K >> 7) / SK), kt_hi = (int)((int64_t)(ks + 1) * (K >> 7) / SK);
   const uint32_t K2 = (uint32_t)K * 2;
   const auto rsX = make_rsrc(x, (uint64_t)M * K2);
   const uint32_t x_voff = (uint32_t)li * K2 + (uint32_t)g * 64;
@@ -73,7 +89,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
       for (int t = 0; t < 4; ++t) xv[mb][t] = buf_load16(rsX, x_voff, mb * 16 * K2 + k * 256 + t * 16);
   };
   if constexpr (!PREW) {
-    for (int kt = wave; kt < KT; kt += nwaves) {
+    for (int kt = kt_lo + wave; kt < kt_hi; kt += nwaves) {
       load_w(kt, wq, sj, zj);
       load_x(kt, xb);
 #pragma unroll
@@ -90,16 +106,16 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
       }
     }
   } else {
-    int kt = wave;
-    if (kt < KT) {
+    int kt = kt_lo + wave;
+    if (kt < kt_hi) {
       load_w(kt, wq, sj, zj);
       load_x(kt, xb);
     }
-    for (; kt < KT; kt += nwaves) {
+    for (; kt < kt_hi; kt += nwaves) {
       const int kn = kt + nwaves;
       uint4 wq2[NB], xb2[MB][4];
       uint32_t sj2[NB], zj2[NB];
-      if (kn < KT) {
+      if (kn < kt_hi) {
         load_w(kn, wq2, sj2, zj2);
         if constexpr (PREX) load_x(kn, xb2);
       }
@@ -115,7 +131,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) acc[j][mb] = mfma16<BF16>(wf[t], xb[mb][t], acc[j][mb]);
       }
-      if (kn < KT) {
+      if (kn < kt_hi) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
           wq[j] = wq2[j];
@@ -134,6 +150,20 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
     }
   }
   // Cross-wave sums, one 16-channel block at a time through the same LDS.
+  // Element e of a block is token m = 16 mb + (l & 15), channel
+  // nn = n0 + 16 j + 4 (l >> 4) + r; with split K it goes to partial slot
+  // ((b * SK + ks) * NB + j) * M * 16 + m * 16 + (nn - n0 - 16 j).
+  auto epilogue = [&](float v, int m, int nn) {
+    if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU || epi == QV_EPI_BIAS_RESID) v += to_f32(bias[nn], BF16);
+    if (epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU) v = gelu_erf(v);
+    if (epi == QV_EPI_BIAS_RESID)  // out + gamma * o, o rounded first (resid_update8)
+      v = to_f32(out[(size_t)m * N + nn], BF16) + to_f32(from_f32<BF16>(v), BF16) * to_f32(gamma[nn], BF16);
+    out[(size_t)m * N + nn] = from_f32<BF16>(v);
+  };
+  const auto rsP = make_rsrc(part, part ? (uint64_t)gridDim.x * SK * NB * M * 16 * 4 : 0);
+  auto slot = [&](int k_split, int j, int m, int c) {
+    return (uint32_t)(((((blockIdx.x * SK + k_split) * NB + j) * M + m) * 16 + c) * 4);
+  };
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     if (j) __syncthreads();
@@ -146,14 +176,28 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
       if (m >= M) continue;
       float v = 0.f;
       for (int w = 0; w < nwaves; ++w) v += red[w][mb][l][r];
-      const int nn = n0 + 16 * j + 4 * (l >> 4) + r;
-      if (epi == QV_EPI_BIAS || epi == QV_EPI_BIAS_GELU || epi == QV_EPI_BIAS_RESID) v += to_f32(bias[nn], BF16);
-      if (epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU) v = gelu_erf(v);
-      if (epi == QV_EPI_BIAS_RESID)  // out + gamma * o, o rounded first (resid_update8)
-        v = to_f32(out[(size_t)m * N + nn], BF16) +
-            to_f32(from_f32<BF16>(v), BF16) * to_f32(gamma[nn], BF16);
-      out[(size_t)m * N + nn] = from_f32<BF16>(v);
+      const int c = 4 * (l >> 4) + r;
+      if (SK == 1)
+        epilogue(v, m, n0 + 16 * j + c);
+      else
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), rsP, slot(ks, j, m, c), 0, 16 /*sc1*/);
     }
+  }
+  if (SK == 1) return;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial values are stored
+  __syncthreads();
+  if (tid == 0) s_arrived = __hip_atomic_fetch_add(cnt + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_arrived != SK - 1) return;   // another split finishes the block
+  if (tid == 0) __hip_atomic_exchange(cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int e = tid; e < M * 16 * NB; e += blockDim.x) {
+    const int m = e / (16 * NB), cn = e % (16 * NB), j = cn >> 4, c = cn & 15;
+    float v = 0.f;
+    for (int k2 = 0; k2 < SK; ++k2) {
+      const float t = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsP, slot(k2, j, m, c), 0, 16));
+      v = k2 == 0 ? t : v + t;
+    }
+    epilogue(v, m, n0 + cn);
   }
 }
 
@@ -282,10 +326,25 @@ static int w4_pick_tile(int M, int N, int K) {
   return best;
 }
 
+// Split-K workspace of the skinny kernel: fp32 partials and one arrival
+// counter per channel block (zero between launches: the finishing split
+// resets it).
+struct SplitWorkspace {
+  float* part = nullptr;
+  int* cnt = nullptr;
+  size_t part_floats = 0;
+  int cnt_n = 0;
+};
+constexpr size_t SPLIT_PART_FLOATS = (size_t)2 << 20;   // 8 MiB of partials
+constexpr int SPLIT_COUNTERS = 4096;                     // channel blocks (N <= 65536)
+
+static int split_workspace(hipStream_t st, SplitWorkspace& ws);
+
 template <bool BF16>
 static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                          void* out, int M, int N, int K, int epi, hipStream_t st,
-                         const void* gamma = nullptr);
+                         const void* gamma = nullptr, const SplitWorkspace* ws = nullptr, int nb_force = 0,
+                         int sk_force = 0);
 
 template <bool BF16>
 static int launch_gemm(const void* x, const void* qw, const void* s, const void* z, const void* bias,
@@ -293,7 +352,12 @@ static int launch_gemm(const void* x, const void* qw, const void* s, const void*
   switch (w4_pick_tile(M, N, K)) {
     case 2: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 96, st);
     case 3: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 64, st);
-    case 5: return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st, gamma);
+    case 5: {
+      SplitWorkspace ws;
+      const int rc = split_workspace(st, ws);
+      if (rc) return rc;
+      return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st, gamma, ws.part ? &ws : nullptr);
+    }
     case 6: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 32, st);
     default: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 128, st);
   }
@@ -308,27 +372,96 @@ static int w4_skinny_nb(int M, int N) {
   return nb;
 }
 
+// Split factor of the skinny kernel: only long K (>= 64 groups) with fewer
+// than 256 channel blocks is split -- 2 ways for M <= 8, else 4 ways with
+// 32-channel blocks, which halves the activation re-reads.  Measured from
+// graph replays over > 1 GB of rotating weights (8192 -> 2048: M = 32
+// 19.9 -> 10.5 us, M = 8 8.1 -> 7.2 us, M = 1 6.4 -> 6.2 us); splitting K <= 2048
+// or shapes that already give >= 256 blocks measured equal or slower.
+static void w4_skinny_plan(int M, int N, int K, const SplitWorkspace* ws, int& nb, int& sk) {
+  nb = w4_skinny_nb(M, N);
+  sk = 1;
+  if (!ws || K / 128 < 64 || N / (16 * nb) >= 256) return;
+  if (M > 8 && N % 32 == 0) {
+    nb = 2;
+    sk = 4;
+  } else {
+    sk = 2;
+  }
+  if ((size_t)N * M * sk > ws->part_floats || N / (16 * nb) > ws->cnt_n) {
+    nb = w4_skinny_nb(M, N);
+    sk = 1;
+  }
+}
+
 template <bool BF16>
 static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                         void* out, int M, int N, int K, int epi, hipStream_t st, const void* gamma) {
-  const int KT = K / 128;
+                         void* out, int M, int N, int K, int epi, hipStream_t st, const void* gamma,
+                         const SplitWorkspace* ws, int nb_force, int sk_force) {
+  int nb, sk;
+  w4_skinny_plan(M, N, K, ws, nb, sk);
+  if (nb_force > 0) nb = nb_force;
+  if (sk_force > 0 && ws) sk = sk_force;
+  const int KT = K / 128 / sk;
   const int waves = KT < 16 ? KT : 16;
-  const int nb = w4_skinny_nb(M, N);
-  const dim3 grid(N / (16 * nb)), block(64 * waves);
+  const dim3 grid(N / (16 * nb), sk), block(64 * waves);
+  float* part = sk > 1 ? ws->part : nullptr;
+  int* cnt = sk > 1 ? ws->cnt : nullptr;
 #define QV_SKINNY(MB, NB)                                                                         \
   hipLaunchKernelGGL((w4a16_skinny_kernel<BF16, MB, NB>), grid, block, 0, st, (const uint16_t*)x, \
                      (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,                 \
-                     (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, epi)
+                     (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, epi, part, cnt)
 #define QV_SKINNY_M(NB)            \
   if (M <= 16) QV_SKINNY(1, NB);   \
   else if (M <= 32) QV_SKINNY(2, NB); \
   else if (M <= 48) QV_SKINNY(3, NB); \
   else QV_SKINNY(4, NB);
-  if (nb == 2) { QV_SKINNY_M(2) }
+  if (nb == 4) { QV_SKINNY_M(4) }
+  else if (nb == 2) { QV_SKINNY_M(2) }
   else { QV_SKINNY_M(1) }
 #undef QV_SKINNY_M
 #undef QV_SKINNY
   return check_launch("w4a16_skinny");
+}
+
+// One split workspace per (device, stream), allocated on first use and
+// zeroed then: launches on one stream run in order and share it; another
+// stream gets its own.  A stream that is being captured into a graph and has
+// none yet gets none (the launch runs unsplit), since allocation is not
+// allowed during capture; the no-allocation entry point covers that case.
+static int split_workspace(hipStream_t st, SplitWorkspace& ws) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, SplitWorkspace> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("w4a16 skinny: hipGetDevice failed");
+    return QV_EHIP;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, st);
+  const auto it = cache.find(key);
+  if (it != cache.end()) {
+    ws = it->second;
+    return QV_OK;
+  }
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    ws = SplitWorkspace();
+    return QV_OK;
+  }
+  SplitWorkspace n;
+  n.part_floats = SPLIT_PART_FLOATS;
+  n.cnt_n = SPLIT_COUNTERS;
+  if (hipMalloc(&n.part, n.part_floats * sizeof(float)) != hipSuccess ||
+      hipMalloc(&n.cnt, n.cnt_n * sizeof(int)) != hipSuccess ||
+      hipMemset(n.cnt, 0, n.cnt_n * sizeof(int)) != hipSuccess) {
+    set_error("w4a16 skinny: split workspace allocation failed (%s)", hipGetErrorString(hipGetLastError()));
+    return QV_EHIP;
+  }
+  cache[key] = n;
+  ws = n;
+  return QV_OK;
 }
 
 static int check_common(const void* x, const void* qw, const void* s, const void* z, const void* bias,
@@ -377,9 +510,15 @@ extern "C" int qv_w4a16_gemv(const void* x, const void* qweight, const void* sca
   // the skinny kernel addresses the activations with 32-bit buffer offsets
   QV_CHECK_ARG(M * K * 2 < ((int64_t)1 << 31), "K=%lld too large for the GEMV", (long long)K);
   hipStream_t st = (hipStream_t)stream;
+  SplitWorkspace ws;
+  rc = split_workspace(st, ws);
+  if (rc) return rc;
+  const SplitWorkspace* w = ws.part ? &ws : nullptr;
   if (dtype == QV_BF16)
-    return launch_skinny<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
-  return launch_skinny<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+    return launch_skinny<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st,
+                               nullptr, w);
+  return launch_skinny<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st,
+                              nullptr, w);
 }
 
 extern "C" int qv_w4a16_dequant(const void* qweight, const void* scales, const void* scaled_zeros,

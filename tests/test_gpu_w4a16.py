@@ -350,3 +350,51 @@ def test_output_must_be_16_byte_aligned(gpu):
                   C.c_void_p(0), ptr(bad), M, N, K, QV_F16, QV_EPI_NONE, C.c_void_p(0))
     torch.cuda.synchronize()
     assert not buf.any()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 2048, 8192), (8, 2048, 8192), (32, 2048, 8192), (40, 1024, 8192),
+                                   (64, 1024, 16384)])
+def test_skinny_split_k(gpu, M, N, K):
+    """Long-K skinny shapes split K across workgroups (fp32 partials, the last
+    split to arrive sums them in split order): parity with the fp32 reference
+    for the plain, bias + GELU and LayerScale-residual epilogues, and bitwise
+    equal re-runs (the sum order does not depend on arrival order)."""
+    from math import erf
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd._lib import QV_EPI_BIAS_GELU
+    p = O.make_w4_problem(M, K, N, seed=M * 31 + K)
+    t = _to_dev(p, gpu)
+    W = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K)
+    ref = O.gemm_ref(p["x"], W)
+    runs = [E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"]) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(runs[0], r) for r in runs[1:])
+    assert O.rel_err(runs[0].float().cpu().numpy(), ref) <= TOL
+    b = (np.random.default_rng(M).standard_normal(N) * 0.3).astype(np.float16)
+    bt = torch.from_numpy(b).to(gpu)
+    y = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=bt, epilogue=QV_EPI_BIAS_GELU)
+    pre = (ref + b.astype(np.float32)).astype(np.float64)
+    gelu = np.vectorize(lambda v: 0.5 * v * (1 + erf(v / np.sqrt(2))))(pre)
+    assert O.rel_err(y.float().cpu().numpy(), gelu) <= TOL
+    gamma = torch.linspace(0.5, 1.5, N, device=gpu).half()
+    resid = torch.randn(M, N, generator=torch.Generator(device=gpu).manual_seed(M), device=gpu).half()
+    o = torch.from_numpy(ref + b.astype(np.float32)).to(gpu).half()   # the linear's fp16 output
+    want = resid.float() + o.float() * gamma.float()
+    got = resid.clone()
+    E.w4a16_linear_residual(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bt, gamma, got)
+    torch.cuda.synchronize()
+    assert ((got.float() - want).abs().max() / want.abs().max()).item() <= TOL
+
+
+def test_skinny_split_k_bf16(gpu):
+    from qvggt_amd import awq_inference_engine as E
+    M, N, K = 24, 2048, 8192
+    p = O.make_w4_problem(M, K, N, seed=23)
+    xb, sc, sz = _bf16_problem(p)
+    x = torch.from_numpy(xb.view(np.int16)).to(gpu).view(torch.bfloat16).view(M, K)
+    qw = torch.from_numpy(p["qweight"]).to(gpu)
+    sct = torch.from_numpy(sc.view(np.int16)).to(gpu).view(torch.bfloat16)
+    szt = torch.from_numpy(sz.view(np.int16)).to(gpu).view(torch.bfloat16)
+    y = E.gemm_forward_cuda_new(x, qw, sct, szt)
+    W = O.bf16_bits_to_f32(O.dequantize_bf16_bits(p["qweight"], sc, sz, N, K))
+    assert O.rel_err(y.float().cpu().numpy(), O.bf16_bits_to_f32(xb) @ W.T) <= TOL
