@@ -98,6 +98,22 @@ int qv_w4a16_gemm_residual(const void* x, const void* qweight, const void* scale
                            void* stream);
 
 /*
+ * qv_w4a16_gemm that allocates nothing: same arguments, kernels, split plan
+ * and bit-identical output.  No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The skinny path's
+ * split-K partials and counters live in a fixed file-scope device array of
+ * 8 MiB + 16 KiB per GPU, held until the process ends; N <= 65536 (larger N
+ * is refused with QV_EINVAL).  The first call on a device resolves the
+ * array's address, so make it outside stream capture.  All calls on one GPU
+ * share the array: calls that overlap (concurrent streams or threads) race.
+ */
+int qv_w4a16_gemm_noalloc(const void* x, const void* qweight, const void* scales,
+                          const void* scaled_zeros, const void* bias, void* out,
+                          int64_t M, int64_t N, int64_t K, int dtype, int epilogue,
+                          void* stream);
+
+/*
  * Quantise + pack: the buffers WQLinear.from_linear stores
  * (awq/qmodule.py:225-329, pack_intweight at qmodule.py:43-99), computed on
  * the GPU.  weight (N, K), scales and zeros (N, K/group_size) in `dtype`

@@ -464,6 +464,48 @@ static int split_workspace(hipStream_t st, SplitWorkspace& ws) {
   return QV_OK;
 }
 
+// ------------------------------------------------- no-allocation variant
+// File-scope device scratch for qv_w4a16_gemm_noalloc: the split partials and
+// counters of SplitWorkspace, fixed at 8 MiB + 16 KiB per GPU for the life of
+// the process.  In host code `scratch` only names the symbol; its device
+// address comes from hipGetSymbolAddress, once per device with that device
+// current (scratch_workspace), and only that address is passed to kernels.
+// Calls that overlap on one GPU share the array and so race.
+static __device__ __align__(256) uint8_t scratch[SPLIT_PART_FLOATS * sizeof(float) + SPLIT_COUNTERS * sizeof(int)];
+
+static int scratch_workspace(SplitWorkspace& ws) {
+  constexpr int MAX_DEV = 64;
+  static std::mutex mu;
+  static void* ptr[MAX_DEV] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) {
+    set_error("w4a16 no-alloc: no usable current device");
+    return QV_EHIP;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("w4a16 no-alloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+      return QV_EHIP;
+    }
+    ptr[dev] = p;
+  }
+  ws.part = reinterpret_cast<float*>(ptr[dev]);
+  ws.cnt = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(ptr[dev]) + SPLIT_PART_FLOATS * sizeof(float));
+  ws.part_floats = SPLIT_PART_FLOATS;
+  ws.cnt_n = SPLIT_COUNTERS;
+  return QV_OK;
+}
+
+// zero n counters (a kernel, not hipMemsetAsync, so the call can be captured
+// into a graph)
+__global__ __launch_bounds__(256) void zero_counters_kernel(int* __restrict__ c, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) c[i] = 0;
+}
+
 static int check_common(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                         const void* out, int64_t M, int64_t N, int64_t K, int dtype, int epi) {
   QV_CHECK_ARG(dtype == QV_F16 || dtype == QV_BF16, "unsupported dtype %d (expected fp16 or bf16)", dtype);
@@ -596,4 +638,37 @@ extern "C" int qv_w4a16_gemm_residual(const void* x, const void* qweight, const 
                              QV_EPI_BIAS_RESID, st, gamma);
   return launch_gemm<false>(x, qweight, scales, scaled_zeros, bias, residual, (int)M, (int)N, (int)K,
                             QV_EPI_BIAS_RESID, st, gamma);
+}
+
+extern "C" int qv_w4a16_gemm_noalloc(const void* x, const void* qweight, const void* scales,
+                                     const void* scaled_zeros, const void* bias, void* out, int64_t M,
+                                     int64_t N, int64_t K, int dtype, int epilogue, void* stream) {
+  int rc = check_common(x, qweight, scales, scaled_zeros, bias, out, M, N, K, dtype, epilogue);
+  if (rc) return rc;
+  QV_CHECK_ARG(N <= (int64_t)SPLIT_COUNTERS * 16,
+               "N=%lld exceeds the no-allocation limit %d (one counter per 16 channels in a fixed scratch)",
+               (long long)N, SPLIT_COUNTERS * 16);
+  if (M == 0) return QV_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (w4_pick_tile((int)M, (int)N, (int)K) != 5) {   // the large-M kernels use no scratch
+    if (dtype == QV_BF16)
+      return launch_gemm<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+    return launch_gemm<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
+  }
+  SplitWorkspace ws;
+  rc = scratch_workspace(ws);
+  if (rc) return rc;
+  int nb, sk;
+  w4_skinny_plan((int)M, (int)N, (int)K, &ws, nb, sk);
+  if (sk > 1) {
+    const int blocks = (int)(N / (16 * nb));
+    hipLaunchKernelGGL(zero_counters_kernel, dim3((blocks + 255) / 256), dim3(256), 0, st, ws.cnt, blocks);
+    rc = check_launch("zero_counters");
+    if (rc) return rc;
+  }
+  if (dtype == QV_BF16)
+    return launch_skinny<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st,
+                               nullptr, &ws);
+  return launch_skinny<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st,
+                              nullptr, &ws);
 }
