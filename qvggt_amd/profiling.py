@@ -7,6 +7,10 @@
     python qvggt_amd/profiling.py camera [--frames S] [--reps R] [--graph]
     python qvggt_amd/profiling.py dense M K N [--bias | --int8]
     python qvggt_amd/profiling.py sdpa [--frames S] [--global]
+    python qvggt_amd/profiling.py rows [--reps R]
+    python qvggt_amd/profiling.py w8a8 M K N [--reps R]
+    python qvggt_amd/profiling.py trace-summary KERNEL_TRACE_CSV [--match NAME] [--grid G] [--run RUN --last N]
+    python qvggt_amd/profiling.py pmc-summary COUNTER_COLLECTION_CSV [--match NAME]
 
 ``copy`` launches one elementwise kernel that reads 512 MiB and writes
 512 MiB, three times: the FETCH_SIZE / WRITE_SIZE it reports per dispatch
@@ -22,7 +26,23 @@ forward.  ``dense`` and ``sdpa`` time the vendor-library counterparts on the
 same shapes, for scale: an unquantised fp16 ``torch.mm`` / ``torch.addmm``
 (hipBLASLt), an int8 x int8 -> int32 ``torch._int_mm`` (hipBLASLt, the W8A8
 counterpart) and torch's ``scaled_dot_product_attention``, each replayed
-from a HIP graph after a 1 s warm-up.  Every mode prints one line when done.
+from a HIP graph after a 1 s warm-up.  ``rows`` runs each HBM-bound row
+kernel at its benchmark shape -- LayerNorm, per-token quant and LN + quant on
+S = 32 tokens (43968 x 1024), GELU + quant on the MLP hidden (10992 x 4096),
+2-D RoPE and qk-norm + 2-D RoPE on the S = 32 qkv (43968 x 3072) -- R times,
+each launch on its own buffer set (so no launch finds its data in the
+caches).  ``w8a8`` runs the W8A8 GEMM with bias (int8 MFMA) on random int8
+operands.  Every mode above prints one line when done.
+
+``trace-summary`` reads a rocprofv3 kernel-trace CSV and prints the dispatch
+count, mean and median duration of the kernels whose name contains NAME
+(and, with ``--grid``, whose grid size in work-items is G).  With ``--run``
+and ``--last N`` it keeps only the last N such dispatches of the first
+uninterrupted run of dispatches whose names contain RUN: for ``bench.py``,
+whose first launches are its MLP steps (pre-warm, warm-up, then the timed
+steps) and nothing else, those are the timed steps.  ``pmc-summary`` reads a
+rocprofv3 ``--pmc`` counter-collection CSV and prints, per kernel (name
+containing NAME) and counter, the value of every dispatch and their mean.
 """
 from __future__ import annotations
 
@@ -134,6 +154,110 @@ def _camera(S, reps, graph):
     print(f"camera: S={S} graph={graph}, {reps} forwards, {ms:.3f} ms per forward", flush=True)
 
 
+def _rows(reps):
+    import numpy as np
+    import torch
+
+    from qvggt_amd import awq_inference_engine as E
+
+    dev = torch.device("cuda:0")
+    f16 = dict(dtype=torch.float16, device=dev)
+    M, D = 32 * 1374, 1024
+    _prewarm()
+    xs = [torch.randn(M, D, **f16) for _ in range(reps)]
+    ys = [torch.empty(M, D, **f16) for _ in range(reps)]
+    q8 = [torch.empty(M, D, dtype=torch.int8, device=dev) for _ in range(reps)]
+    sc = [torch.empty(M, **f16) for _ in range(reps)]
+    g, b = torch.ones(D, **f16), torch.zeros(D, **f16)
+    for i in range(reps):
+        E.layer_norm(xs[i], g, b, 1e-6, out=ys[i])
+    for i in range(reps):
+        E.invoke_quant(q8[i], xs[i], sc[i])
+    for i in range(reps):
+        E.rms_norm_general(q8[i], xs[i], g, b, sc[i], 1e-6, True)
+    torch.cuda.synchronize()
+    del xs, ys, q8, sc
+    Mh, Dh = 8 * 1374, 4096
+    for i in range(reps):
+        hx = torch.randn(Mh, Dh, **f16)
+        hq = torch.empty(Mh, Dh, dtype=torch.int8, device=dev)
+        ht = torch.empty(Mh, Dh, **f16)
+        E.gelu_and_quant(hq, hx, torch.empty(Mh, **f16), ht)
+        torch.cuda.synchronize()
+    del hx, hq, ht
+    pos = torch.from_numpy(np.tile(np.array([[0, 0]] * 5 + [[i // 37 + 1, i % 37 + 1] for i in range(1369)],
+                                            np.int32), (32, 1))).to(dev)
+    ct, st = E.rope2d_tables(38, device=dev)
+    qkv = [torch.randn(M, 3 * D, **f16) for _ in range(reps)]
+    for i in range(reps):
+        E.rope2d(qkv[i], pos, ct, st, 16, out=qkv[i])
+    gq, bq = torch.ones(64, **f16), torch.zeros(64, **f16)
+    for i in range(reps):
+        E.qknorm_rope2d(qkv[i], pos, ct, st, 16, gq, bq, gq, bq)
+    torch.cuda.synchronize()
+    print(f"rows: layernorm, quant, ln+quant (S=32), gelu+quant (10992x4096), rope2d, qknorm_rope2d (S=32), "
+          f"{reps} launches each", flush=True)
+
+
+def _w8a8(M, K, N, reps):
+    import torch
+
+    from qvggt_amd import awq_inference_engine as E
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+    w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+    ws = (torch.rand(N, generator=g) * 0.01).half().to(dev)
+    as_ = (torch.rand(M, generator=g) * 0.01).half().to(dev)
+    b = torch.zeros(N, dtype=torch.float16, device=dev)
+    o = torch.empty(M, N, dtype=torch.float16, device=dev)
+    _prewarm()
+    for _ in range(reps):
+        E.w8a8_gemm_fuse_bias_forward_cuda(a, w, ws, as_, o, b)
+    torch.cuda.synchronize()
+    print(f"w8a8: M={M} K={K} N={N} + bias, {reps} launches", flush=True)
+
+
+def _trace_summary(path, match, grid, run, last):
+    import csv
+    import statistics
+
+    with open(path, newline="") as f:
+        rows = list(csv.DictReader(f))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+
+    def hit(r):
+        return match in r["Kernel_Name"] and (grid is None or int(r["Grid_Size"]) == grid)
+
+    if run:
+        first = next(i for i, r in enumerate(rows) if run in r["Kernel_Name"])
+        end = next((i for i in range(first, len(rows)) if run not in rows[i]["Kernel_Name"]), len(rows))
+        rows = rows[first:end]
+    sel = [r for r in rows if hit(r)]
+    if last:
+        sel = sel[-last:]
+    us = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in sel]
+    names = sorted({r["Kernel_Name"] for r in sel})
+    print(f"{len(us)} dispatches of {names}: mean {statistics.mean(us):.2f} us, "
+          f"median {statistics.median(us):.2f} us, min {min(us):.2f}, max {max(us):.2f}", flush=True)
+
+
+def _pmc_summary(path, match):
+    import csv
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(float))   # (kernel, counter) -> dispatch -> value
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if match in r["Kernel_Name"]:
+                vals[(r["Kernel_Name"], r["Counter_Name"])][int(r["Dispatch_Id"])] += float(r["Counter_Value"])
+    for (name, ctr), d in sorted(vals.items()):
+        v = [d[k] for k in sorted(d)]
+        print(f"{name.split('(')[0]} | {ctr} | dispatches {len(v)} | mean {sum(v) / len(v):.6g} | "
+              f"values {', '.join(f'{x:.6g}' for x in v)}", flush=True)
+
+
 def _replay_us(fn, reps=20, rounds=5):
     import time
 
@@ -223,6 +347,22 @@ def main(argv=None):
     q = sub.add_parser("sdpa")
     q.add_argument("--frames", type=int, default=8)
     q.add_argument("--global", dest="glob", action="store_true")
+    r = sub.add_parser("rows")
+    r.add_argument("--reps", type=int, default=3)
+    w = sub.add_parser("w8a8")
+    w.add_argument("M", type=int)
+    w.add_argument("K", type=int)
+    w.add_argument("N", type=int)
+    w.add_argument("--reps", type=int, default=3)
+    ts = sub.add_parser("trace-summary")
+    ts.add_argument("csv")
+    ts.add_argument("--match", default="")
+    ts.add_argument("--grid", type=int, default=None)
+    ps = sub.add_parser("pmc-summary")
+    ps.add_argument("csv")
+    ps.add_argument("--match", default="")
+    ts.add_argument("--run", default="")
+    ts.add_argument("--last", type=int, default=0)
     args = ap.parse_args(argv)
     if args.mode == "copy":
         _copy()
@@ -236,6 +376,14 @@ def main(argv=None):
         _dense(args.M, args.K, args.N, args.bias, args.int8)
     elif args.mode == "sdpa":
         _sdpa(args.frames, args.glob)
+    elif args.mode == "rows":
+        _rows(args.reps)
+    elif args.mode == "w8a8":
+        _w8a8(args.M, args.K, args.N, args.reps)
+    elif args.mode == "pmc-summary":
+        _pmc_summary(args.csv, args.match)
+    elif args.mode == "trace-summary":
+        _trace_summary(args.csv, args.match, args.grid, args.run, args.last)
     else:
         _aggregator(args.frames, args.w8a8)
 
