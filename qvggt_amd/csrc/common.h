@@ -96,6 +96,17 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return __builtin_fmaf(-a, __builtin_amdgcn_exp2f(p), __builtin_fmaxf(v, 0.0f));
 }
 
+// Byte offset of (row, byte) in a GEMM epilogue staging area of 128-byte rows
+// (a wave's 64-channel fp16 output tile): 16-byte chunk c of row r sits at
+// c ^ ((r >> 1) & 7).  The staging writes (8 bytes, one row per lane, the same
+// column) and the row read-back (16 bytes, eight lanes per row) then each put
+// the lanes of a 16-lane group on distinct banks; with unswizzled rows padded to
+// 144 bytes the SQ_LDS_BANK_CONFLICT counter read ~0.5 conflict cycles per LDS
+// instruction of the W4A16 GEMM.
+__device__ __forceinline__ uint32_t stg_off(int row, int byte) {
+  return (uint32_t)(row * 128 + ((((byte >> 4) ^ (row >> 1)) & 7) << 4) + (byte & 15));
+}
+
 // Raw buffer descriptor (gfx9 dword3 = 32-bit data format) over `bytes`
 // bytes from `base`; loads at offsets >= bytes return zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {

@@ -19,7 +19,7 @@
 // operands (activations: 8 contiguous halves of chunk 4h + s).  Output: lane
 // (h, l), register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the tile.
 // LDS per workgroup: max(3 stages x BM*128, the epilogue staging of 4 x BM x
-// 144 B); BM = 128 -> 72 KB, 2 workgroups/CU.  The epilogue stages each wave's
+// 128 B); BM = 128 -> 64 KB, 2 workgroups/CU.  The epilogue stages each wave's
 // BM x 64 output tile there and writes it back as whole 128-byte rows.
 #include "w4a16_common.h"
 
@@ -38,7 +38,7 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
   constexpr int NSTAGE = 3;
   constexpr int A_INSTR = BM / 32;                // 1 KB direct loads per wave for A
   static_assert(A_INSTR < 16, "vmcnt immediate");
-  constexpr int EP = 144;  // bytes per staged epilogue row: 64 fp16 + 16 B pad
+  constexpr int EP = 128;  // bytes per staged epilogue row (64 fp16, chunk-swizzled: stg_off)
   constexpr int LDS_BYTES = NSTAGE * STAGE > 4 * BM * EP ? NSTAGE * STAGE : 4 * BM * EP;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
@@ -205,7 +205,7 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
         uint2 o;
         o.x = pack2<BF16>(r[0], r[1]);
         o.y = pack2<BF16>(r[2], r[3]);
-        *reinterpret_cast<uint2*>(stg + (32 * i + l32) * EP + nl * 2) = o;
+        *reinterpret_cast<uint2*>(stg + stg_off(32 * i + l32, nl * 2)) = o;
       }
     }
   }
@@ -217,7 +217,7 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
     const int row = idx >> 3, c = idx & 7;
     const int m = m0 + row, n = n0 + 64 * wave + 8 * c;
     if (m < M && n < N) {
-      uint4 v = *reinterpret_cast<const uint4*>(stg + row * EP + c * 16);
+      uint4 v = *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16));
       if constexpr (EPI == QV_EPI_BIAS_RESID)
         v = resid_update8<BF16>(*reinterpret_cast<const uint4*>(out + (size_t)m * N + n), v,
                                 *reinterpret_cast<const uint4*>(gamma + n));
