@@ -71,7 +71,42 @@ __device__ __forceinline__ uint16_t from_f32(float v) {
 
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return (uint32_t)from_f32<BF16>(a) | ((uint32_t)from_f32<BF16>(b) << 16);
+  if constexpr (BF16) {
+    return (uint32_t)from_f32<true>(a) | ((uint32_t)from_f32<true>(b) << 16);
+  } else {
+    // gfx950's v_cvt_pk_f16_f32 rounds both halves to nearest even like two
+    // v_cvt_f16_f32, in one instruction (inline asm: no fusion with the
+    // producer either)
+    uint32_t r;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+  }
+}
+
+// v_fma_mix_f32 with 16-bit float operands taken from half K (0 = low, 1 =
+// high) of a 32-bit register: the fp16 -> fp32 conversion is exact and free,
+// and each result is the exact value rounded once to fp32, so these equal
+// the conversion followed by the plain fp32 operation bit for bit.
+template <int K>
+__device__ __forceinline__ float mix_add(uint32_t h2, float c) {  // float(h) + c
+  float d;
+  if constexpr (K == 0) asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h2), "v"(c));
+  else asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h2), "v"(c));
+  return d;
+}
+template <int K>
+__device__ __forceinline__ float mix_sq_add(uint32_t h2, float c) {  // float(h)^2 + c (the square is exact)
+  float d;
+  if constexpr (K == 0) asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel_hi:[1,1,0]" : "=v"(d) : "v"(h2), "v"(c));
+  else asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(d) : "v"(h2), "v"(c));
+  return d;
+}
+template <int K>
+__device__ __forceinline__ float mix_mul(float a, uint32_t h2) {  // a * float(h), as a * h + (-0)
+  float d;
+  if constexpr (K == 0) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(d) : "v"(a), "v"(h2), "v"(-0.0f));
+  else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(d) : "v"(a), "v"(h2), "v"(-0.0f));
+  return d;
 }
 
 // GELU with the exact-erf definition of torch.nn.GELU(), 0.5 v (1 + erf(v / sqrt 2))
