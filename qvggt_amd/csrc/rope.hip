@@ -146,11 +146,15 @@ template <int NR>
 __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
     uint16_t* __restrict__ qkv, const int* __restrict__ pos, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, int P, const uint16_t* __restrict__ qg, const uint16_t* __restrict__ qb,
-    const uint16_t* __restrict__ kg, const uint16_t* __restrict__ kb, float eps, int T, int H, long tok_stride) {
+    const uint16_t* __restrict__ kg, const uint16_t* __restrict__ kb, float eps, int T, int H, long tok_stride,
+    int hshift) {
   const long nrows = (long)T * 2 * H;
   const long g0 = (long)blockIdx.x * (QKN_ROWS_PER_WG * NR) + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
-  float x[NR][8];
+  // the row's 8 fp16 values stay packed (pairs 2m, 2m+1 in word m) and enter
+  // the fp32 arithmetic through v_fma_mix_f32 (mix_add / mix_mul), which
+  // converts exactly for free: the same values as converting first
+  uint32_t xw[NR][4];
   bool live[NR];
   int tokv[NR], partv[NR];
   uint16_t* row[NR];
@@ -159,60 +163,73 @@ __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
     const long r = g0 + QKN_ROWS_PER_WG * k;
     live[k] = r < nrows;
     const long rc = live[k] ? r : 0;          // dead lanes shadow row 0 and store nothing
-    const int tok = (int)(rc / (2 * H));
-    const int rr = (int)(rc % (2 * H));
-    const int part = rr / H, head = rr % H;
+    int tok, part, head;
+    if (hshift >= 0) {                        // H = 2^hshift: shifts instead of 64-bit divisions
+      tok = (int)(rc >> (hshift + 1));
+      part = (int)(rc >> hshift) & 1;
+      head = (int)rc & ((1 << hshift) - 1);
+    } else {
+      tok = (int)(rc / (2 * H));
+      const int rr = (int)(rc % (2 * H));
+      part = rr / H;
+      head = rr % H;
+    }
     tokv[k] = tok;
     partv[k] = part;
     row[k] = qkv + (size_t)tok * tok_stride + (size_t)part * H * 64 + (size_t)head * 64;
-    const f16x8 v = __builtin_bit_cast(f16x8, ld_stream16(row[k] + 8 * j));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[k][e] = (float)v[e];
+    const uint4 v = ld_stream16(row[k] + 8 * j);
+    xw[k][0] = v.x; xw[k][1] = v.y; xw[k][2] = v.z; xw[k][3] = v.w;
   }
   const int half = j >> 2;
   const int i0 = 8 * (j & 1);
   const bool lo = (j & 2) == 0;
   // q and k norm weights for this lane's 8 dims, fetched with the rows rather
   // than after the statistics
-  const f16x8 gqv = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(qg)[j]);
-  const f16x8 bqv = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(qb)[j]);
-  const f16x8 gkv = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(kg)[j]);
-  const f16x8 bkv = __builtin_bit_cast(f16x8, reinterpret_cast<const uint4*>(kb)[j]);
+  const uint4 gq = reinterpret_cast<const uint4*>(qg)[j], bq = reinterpret_cast<const uint4*>(qb)[j];
+  const uint4 gk = reinterpret_cast<const uint4*>(kg)[j], bk = reinterpret_cast<const uint4*>(kb)[j];
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
     float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s = s + x[k][e];
-    const float mean = sum8_lanes(s) / 64.0f;
-    float s2 = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      x[k][e] = x[k][e] - mean;
-      s2 = s2 + x[k][e] * x[k][e];
+    for (int m = 0; m < 4; ++m) {
+      s = mix_add<0>(xw[k][m], s);
+      s = mix_add<1>(xw[k][m], s);
     }
+    const float nm = -(sum8_lanes(s) / 64.0f);
+    float d[8], s2 = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      d[2 * m] = mix_add<0>(xw[k][m], nm);
+      d[2 * m + 1] = mix_add<1>(xw[k][m], nm);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s2 = s2 + d[e] * d[e];
     const float rs = 1.0f / __builtin_sqrtf(sum8_lanes(s2) / 64.0f + eps);
-    const f16x8 g = partv[k] ? gkv : gqv;
-    const f16x8 b = partv[k] ? bkv : bqv;
+    const uint4 g = partv[k] ? gk : gq;
+    const uint4 b = partv[k] ? bk : bq;
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, bw[4] = {b.x, b.y, b.z, b.w};
+    uint32_t yw[4];   // q_norm / k_norm output, rounded to fp16
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float t = (x[k][e] * rs) * (float)g[e] + (float)b[e];
-      x[k][e] = (float)__builtin_bit_cast(_Float16, from_f32<false>(t));   // q_norm output is fp16
-    }
+    for (int m = 0; m < 4; ++m)
+      yw[m] = pack2<false>(mix_add<0>(bw[m], mix_mul<0>(d[2 * m] * rs, gw[m])),
+                           mix_add<1>(bw[m], mix_mul<1>(d[2 * m + 1] * rs, gw[m])));
     int p = pos[2 * tokv[k] + half];
     p = p < 0 ? 0 : (p >= P ? P - 1 : p);
     const float4* cp = reinterpret_cast<const float4*>(cos_t + p * 16 + i0);
     const float4* sp = reinterpret_cast<const float4*>(sin_t + p * 16 + i0);
     const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
     const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    f16x8 o;
+    // the first of a rotation pair subtracts the partner term: x*c - o*s = x*c + o*(-s)
+    const float sg = lo ? -1.0f : 1.0f;
+    const float sn[8] = {sg * s0.x, sg * s0.y, sg * s0.z, sg * s0.w, sg * s1.x, sg * s1.y, sg * s1.z, sg * s1.w};
+    uint32_t ow[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float other = dpp_f<0x4E>(x[k][e]);   // partner lane j ^ 2
-      const float v = lo ? x[k][e] * cs[e] - other * sn[e] : x[k][e] * cs[e] + other * sn[e];
-      o[e] = __builtin_bit_cast(_Float16, from_f32<false>(v));
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)yw[m], 0x4E, 0xF, 0xF, true);  // lane j ^ 2
+      ow[m] = pack2<false>(mix_mul<0>(cs[2 * m], yw[m]) + mix_mul<0>(sn[2 * m], other),
+                           mix_mul<1>(cs[2 * m + 1], yw[m]) + mix_mul<1>(sn[2 * m + 1], other));
     }
-    if (live[k]) st_stream16(row[k] + 8 * j, __builtin_bit_cast(uint4, o));
+    if (live[k]) st_stream16(row[k] + 8 * j, make_uint4(ow[0], ow[1], ow[2], ow[3]));
   }
 }
 
@@ -241,7 +258,8 @@ extern "C" int qv_qknorm_rope2d(void* qkv, const int32_t* positions, const float
                      dim3((unsigned)((rows + QKN_ROWS_PER_WG * NR - 1) / (QKN_ROWS_PER_WG * NR))), dim3(256), 0,
                      (hipStream_t)stream, (uint16_t*)qkv, positions, cos_table, sin_table, (int)table_rows,
                      (const uint16_t*)q_gamma, (const uint16_t*)q_beta, (const uint16_t*)k_gamma,
-                     (const uint16_t*)k_beta, eps, (int)T, (int)H, (long)token_stride);
+                     (const uint16_t*)k_beta, eps, (int)T, (int)H, (long)token_stride,
+                     (H & (H - 1)) == 0 ? __builtin_ctzll((unsigned long long)H) : -1);
   return check_launch("qknorm_rope2d");
 }
 
