@@ -88,11 +88,11 @@ template <int NR>
 __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                           const int* __restrict__ pos, const float* __restrict__ cos_t,
                                                           const float* __restrict__ sin_t, int P, int T, int H,
-                                                          long src_tok, long dst_tok, long dst_part) {
+                                                          long src_tok, long dst_tok, long dst_part, int hshift) {
   const long nrows = (long)T * 2 * H;
   const long g0 = (long)blockIdx.x * (32 * NR) + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
-  f16x8 x[NR];
+  uint32_t xw[NR][4];   // the row's 8 fp16 values, packed (read through v_fma_mix_f32)
   bool live[NR];
   int tokv[NR];
   long doff[NR];
@@ -101,12 +101,21 @@ __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict_
     const long r = g0 + 32 * k;
     live[k] = r < nrows;
     const long rc = live[k] ? r : 0;
-    const int tok = (int)(rc / (2 * H));
-    const int rr = (int)(rc % (2 * H));
-    const int part = rr / H, head = rr % H;
+    int tok, part, head;
+    if (hshift >= 0) {                        // H = 2^hshift: shifts instead of 64-bit divisions
+      tok = (int)(rc >> (hshift + 1));
+      part = (int)(rc >> hshift) & 1;
+      head = (int)rc & ((1 << hshift) - 1);
+    } else {
+      tok = (int)(rc / (2 * H));
+      const int rr = (int)(rc % (2 * H));
+      part = rr / H;
+      head = rr % H;
+    }
     tokv[k] = tok;
     doff[k] = (long)tok * dst_tok + (long)part * dst_part + (long)head * 64 + 8 * j;
-    x[k] = __builtin_bit_cast(f16x8, ld_stream16(src + (size_t)tok * src_tok + (size_t)part * H * 64 + (size_t)head * 64 + 8 * j));
+    const uint4 v = ld_stream16(src + (size_t)tok * src_tok + (size_t)part * H * 64 + (size_t)head * 64 + 8 * j);
+    xw[k][0] = v.x; xw[k][1] = v.y; xw[k][2] = v.z; xw[k][3] = v.w;
   }
   const int half = j >> 2;
   const int i0 = 8 * (j & 1);
@@ -119,16 +128,17 @@ __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict_
     const float4* sp = reinterpret_cast<const float4*>(sin_t + p * 16 + i0);
     const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
     const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    f16x8 o;
+    // the first of a rotation pair subtracts the partner term: x*c - o*s = x*c + o*(-s)
+    const float sg = lo ? -1.0f : 1.0f;
+    const float sn[8] = {sg * s0.x, sg * s0.y, sg * s0.z, sg * s0.w, sg * s1.x, sg * s1.y, sg * s1.z, sg * s1.w};
+    uint32_t ow[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float xv = (float)x[k][e];
-      const float other = dpp_f<0x4E>(xv);
-      const float v = lo ? xv * cs[e] - other * sn[e] : xv * cs[e] + other * sn[e];
-      o[e] = (_Float16)v;
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)xw[k][m], 0x4E, 0xF, 0xF, true);  // lane j ^ 2
+      ow[m] = pack2<false>(mix_mul<0>(cs[2 * m], xw[k][m]) + mix_mul<0>(sn[2 * m], other),
+                           mix_mul<1>(cs[2 * m + 1], xw[k][m]) + mix_mul<1>(sn[2 * m + 1], other));
     }
-    if (live[k]) st_stream16(dst + doff[k], __builtin_bit_cast(uint4, o));
+    if (live[k]) st_stream16(dst + doff[k], make_uint4(ow[0], ow[1], ow[2], ow[3]));
   }
 }
 
@@ -312,6 +322,6 @@ extern "C" int qv_rope2d(const void* qkv, void* out, const int32_t* positions, c
   hipLaunchKernelGGL(rope2d_kernel<NR>, dim3((unsigned)((nrows + 32 * NR - 1) / (32 * NR))), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)qkv, (uint16_t*)out, positions, cos_table, sin_table,
                      (int)table_rows, (int)T, (int)H, (long)src_token_stride, (long)dst_token_stride,
-                     (long)dst_part_stride);
+                     (long)dst_part_stride, (H & (H - 1)) == 0 ? __builtin_ctzll((unsigned long long)H) : -1);
   return check_launch("rope2d");
 }

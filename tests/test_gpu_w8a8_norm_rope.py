@@ -299,10 +299,12 @@ def test_fused_rope_with_pos(gpu, transpose_out, dt):
         assert np.abs(got - ref).max() <= 2e-6 * max(1.0, np.abs(ref).max())
 
 
-@pytest.mark.parametrize("inplace", [False, True])
-def test_rope2d_bit_exact(gpu, inplace):
+@pytest.mark.parametrize("inplace,H", [(False, 16), (True, 16), (False, 6), (True, 1)])
+def test_rope2d_bit_exact(gpu, inplace, H):
+    """H = 16 (a power of two) takes the kernel's shift-based row indexing,
+    H = 6 the division path; H = 1 is the smallest power of two."""
     from qvggt_amd import awq_inference_engine as E
-    S, H = 2, 16
+    S = 2
     pos = R.vggt_positions(S)
     T = pos.shape[0]
     qkv = _rng(4).standard_normal((T, 3 * H * 64)).astype(np.float16)
@@ -323,9 +325,10 @@ def test_rope2d_bit_exact(gpu, inplace):
         assert np.array_equal(got[:, part].view(np.int16), ref.view(np.int16))
 
 
-def test_qknorm_rope2d_bit_exact(gpu):
+@pytest.mark.parametrize("H", [16, 6])
+def test_qknorm_rope2d_bit_exact(gpu, H):
     from qvggt_amd import awq_inference_engine as E
-    S, H = 2, 16
+    S = 2
     pos = R.vggt_positions(S)
     T = pos.shape[0]
     rng = _rng(11)
