@@ -98,6 +98,27 @@ int qv_w4a16_gemm_residual(const void* x, const void* qweight, const void* scale
                            void* stream);
 
 /*
+ * The VGGT qkv projection fused with what follows it: out (M, 3*H*64) =
+ * fp16(x @ W^T + bias), then for every token the per-head LayerNorm of the q
+ * and k heads (q_gamma/q_beta, k_gamma/k_beta (64) fp16, eps) rounded to
+ * fp16, then the VGGT 2-D RoPE of qv_qknorm_rope2d (positions int32 (M, 2),
+ * fp32 cos/sin tables (table_rows, 16)); the v heads get the bias only.
+ * fp16 only.  The reference has no single op for this: it is
+ * WQLinear.forward (qmodule.py:331-369, gemm_forward_cuda_new) followed by
+ * vggt-hf's q_norm / k_norm and RoPE, i.e. qv_w4a16_gemm then
+ * qv_qknorm_rope2d, which this entry replaces with one kernel for M > 64
+ * (for M <= 64 it runs exactly those two).  The LayerNorm statistics are
+ * summed in another order than qv_qknorm_rope2d's, so the q and k outputs
+ * may differ from the two-step path in the last bit.
+ */
+int qv_w4a16_gemm_qkrope(const void* x, const void* qweight, const void* scales,
+                         const void* scaled_zeros, const void* bias, void* out,
+                         int64_t M, int64_t N, int64_t K, const int32_t* positions,
+                         const float* cos_table, const float* sin_table, int64_t table_rows,
+                         const void* q_gamma, const void* q_beta, const void* k_gamma,
+                         const void* k_beta, float eps, int64_t H, void* stream);
+
+/*
  * qv_w4a16_gemm that allocates nothing: same arguments, kernels, split plan
  * and bit-identical output.  No counterpart in the reference; it is for
  * callers that cannot allocate device memory (code under HIP graph capture,

@@ -275,14 +275,21 @@ class AABlock(nn.Module):
         M = x.shape[0]
         a = self.attn
         eps = self.eps
-        if not self.w8a8:
+        if not self.w8a8 and isinstance(a.qkv, WQLinear) and a.qkv.bias is not None:
+            # the qkv projection with its q/k LayerNorm and 2-D RoPE in the GEMM epilogue
             h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, eps, out=ws["h"])
-            qkv = _linear(a.qkv, h, QV_EPI_BIAS, ws["qkv"])
+            qkv = E.w4a16_linear_qkrope(h, a.qkv.qweight, a.qkv.scales, a.qkv.scaled_zeros, a.qkv.bias, pos,
+                                        tables[0], tables[1], HEADS, a.q_norm.weight, a.q_norm.bias,
+                                        a.k_norm.weight, a.k_norm.bias, eps, out=ws["qkv"])
         else:
-            E.rms_norm_general(ws["q8"], x, self.norm1.weight, self.norm1.bias, ws["s8"], eps, True)
-            qkv = a.qkv(ws["q8"], ws["s8"], out=ws["qkv"])
-        E.qknorm_rope2d(qkv, pos, tables[0], tables[1], HEADS, a.q_norm.weight, a.q_norm.bias,
-                        a.k_norm.weight, a.k_norm.bias, eps)
+            if not self.w8a8:
+                h = E.layer_norm(x, self.norm1.weight, self.norm1.bias, eps, out=ws["h"])
+                qkv = _linear(a.qkv, h, QV_EPI_BIAS, ws["qkv"])
+            else:
+                E.rms_norm_general(ws["q8"], x, self.norm1.weight, self.norm1.bias, ws["s8"], eps, True)
+                qkv = a.qkv(ws["q8"], ws["s8"], out=ws["qkv"])
+            E.qknorm_rope2d(qkv, pos, tables[0], tables[1], HEADS, a.q_norm.weight, a.q_norm.bias,
+                            a.k_norm.weight, a.k_norm.bias, eps)
         v3 = qkv.view(M, 3, HEADS, HEAD_DIM)
         att = E.attention(v3[:, 0], v3[:, 1], v3[:, 2], seq_len, out=ws["att"].view(M, HEADS, HEAD_DIM))
         att = att.view(M, DIM)

@@ -169,6 +169,50 @@ def w4a16_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+def w4a16_linear_qkrope(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
+                        scaled_zeros: torch.Tensor, bias: torch.Tensor, positions: torch.Tensor,
+                        cos_table: torch.Tensor, sin_table: torch.Tensor, heads: int,
+                        q_gamma: torch.Tensor, q_beta: torch.Tensor, k_gamma: torch.Tensor,
+                        k_beta: torch.Tensor, eps: float = 1e-6, out: torch.Tensor | None = None) -> torch.Tensor:
+    """A VGGT block's qkv projection with its q/k LayerNorm and 2-D RoPE fused
+    into the GEMM epilogue (fp16): the result of ``w4a16_linear(..., bias,
+    QV_EPI_BIAS)`` followed by ``qknorm_rope2d`` in one kernel for M > 64 (the
+    two calls themselves for smaller M).  Returns out (..., 3*heads*64)."""
+    what = "w4a16_linear_qkrope"
+    if x.dtype != torch.float16:
+        _fail(f"{what}: x must be float16")
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    N = qweight.shape[0] * 4
+    if N != 3 * heads * 64:
+        _fail(f"{what}: the projection must have 3*heads*64 = {3 * heads * 64} outputs, got {N}")
+    _check_w4_tables(qweight, scales, scaled_zeros, N, K, x.dtype, what)
+    if bias is None or bias.dtype != x.dtype or bias.numel() != N:
+        _fail(f"{what}: bias must be ({N},) {x.dtype}")
+    for name, t in (("q_gamma", q_gamma), ("q_beta", q_beta), ("k_gamma", k_gamma), ("k_beta", k_beta)):
+        if t.dtype != torch.float16 or t.numel() != 64:
+            _fail(f"{what}: {name} must be float16 (64,)")
+    if positions.dtype != torch.int32 or positions.numel() != 2 * M:
+        _fail(f"{what}: positions must be int32 (M, 2)")
+    _check_rope_tables(cos_table, sin_table, what)
+    if out is not None:
+        _check_out(out, M, N, x.dtype, what)
+    dev = _on_gpu(x, qweight, scales, scaled_zeros, bias, positions, cos_table, sin_table, q_gamma, q_beta,
+                  k_gamma, k_beta, out, what=what)
+    x = _contig(x)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=dev)
+    # contiguous copies bound to names: they must outlive the native call
+    qw, sc, sz, bb = _contig(qweight), _contig(scales), _contig(scaled_zeros), _contig(bias)
+    pos = _contig(positions)
+    qg, qb, kg, kb = _contig(q_gamma), _contig(q_beta), _contig(k_gamma), _contig(k_beta)
+    with _device(dev):
+        _lib.call("qv_w4a16_gemm_qkrope", _ptr(x), _ptr(qw), _ptr(sc), _ptr(sz), _ptr(bb), _ptr(out), M, N, K,
+                  _ptr(pos), _ptr(cos_table), _ptr(sin_table), cos_table.shape[0], _ptr(qg), _ptr(qb), _ptr(kg),
+                  _ptr(kb), C.c_float(eps), heads, _stream(dev))
+    return out
+
+
 def w4a16_linear_residual(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
                           scaled_zeros: torch.Tensor, bias: torch.Tensor, gamma: torch.Tensor,
                           residual: torch.Tensor) -> torch.Tensor:

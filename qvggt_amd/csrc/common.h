@@ -131,6 +131,15 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return __builtin_fmaf(-a, __builtin_amdgcn_exp2f(p), __builtin_fmaxf(v, 0.0f));
 }
 
+// {v[l], v[l ^ 32]} in some order in a and b (v_permlane32_swap with both
+// operands holding v): a + b or max(a, b) is the 32-apart butterfly step.
+// Inline asm with the VALU -> permlane hazard covered by s_nop.
+__device__ __forceinline__ void pair32(float v, float& a, float& b) {
+  a = v;
+  b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
 // Byte offset of (row, byte) in a GEMM epilogue staging area of 128-byte rows
 // (a wave's 64-channel fp16 output tile): 16-byte chunk c of row r sits at
 // c ^ ((r >> 1) & 7).  The staging writes (8 bytes, one row per lane, the same

@@ -640,6 +640,49 @@ extern "C" int qv_w4a16_gemm_residual(const void* x, const void* qweight, const 
                             QV_EPI_BIAS_RESID, st, gamma);
 }
 
+extern "C" int qv_w4a16_gemm_qkrope(const void* x, const void* qweight, const void* scales,
+                                    const void* scaled_zeros, const void* bias, void* out, int64_t M, int64_t N,
+                                    int64_t K, const int32_t* positions, const float* cos_table,
+                                    const float* sin_table, int64_t table_rows, const void* q_gamma,
+                                    const void* q_beta, const void* k_gamma, const void* k_beta, float eps,
+                                    int64_t H, void* stream) {
+  int rc = check_common(x, qweight, scales, scaled_zeros, bias, out, M, N, K, QV_F16, QV_EPI_BIAS);
+  if (rc) return rc;
+  QV_CHECK_ARG(bias != nullptr, "the fused q/k-norm + RoPE projection needs its bias");
+  QV_CHECK_ARG(H > 0 && N == 3 * H * 64, "N=%lld must be 3 x heads x 64 (heads=%lld)", (long long)N, (long long)H);
+  QV_CHECK_ARG(table_rows > 0 && table_rows <= INT32_MAX, "bad table_rows %lld", (long long)table_rows);
+  QV_CHECK_ARG(positions && cos_table && sin_table && q_gamma && q_beta && k_gamma && k_beta,
+               "null pointer argument");
+  QV_CHECK_ARG(((uintptr_t)cos_table % 16) == 0 && ((uintptr_t)sin_table % 16) == 0 &&
+                   ((uintptr_t)positions % 8) == 0,
+               "cos/sin tables must be 16-byte and positions 8-byte aligned");
+  QV_CHECK_ARG(((uintptr_t)q_gamma % 16) == 0 && ((uintptr_t)q_beta % 16) == 0 && ((uintptr_t)k_gamma % 16) == 0 &&
+                   ((uintptr_t)k_beta % 16) == 0,
+               "norm weights must be 16-byte aligned");
+  if (M == 0) return QV_OK;
+  const int tile = w4_pick_tile((int)M, (int)N, (int)K);
+  if (tile == 5) {  // skinny M: the projection, then the standalone q/k-norm + RoPE pass
+    rc = qv_w4a16_gemm(x, qweight, scales, scaled_zeros, bias, out, M, N, K, QV_F16, QV_EPI_BIAS, stream);
+    if (rc) return rc;
+    return qv_qknorm_rope2d(out, positions, cos_table, sin_table, table_rows, q_gamma, q_beta, k_gamma, k_beta,
+                            eps, M, H, N, stream);
+  }
+  QkRopeArgs a;
+  a.pos = positions;
+  a.cos_t = cos_table;
+  a.sin_t = sin_table;
+  a.qg = (const uint16_t*)q_gamma;
+  a.qb = (const uint16_t*)q_beta;
+  a.kg = (const uint16_t*)k_gamma;
+  a.kb = (const uint16_t*)k_beta;
+  a.P = (int)table_rows;
+  a.qk_cols = (int)(2 * H * 64);
+  a.eps = eps;
+  const int bm = tile == 2 ? 96 : (tile == 3 ? 64 : (tile == 6 ? 32 : 128));
+  return launch_w4a16_stream<false>(x, qweight, scales, scaled_zeros, bias, nullptr, out, (int)M, (int)N, (int)K,
+                                    QV_EPI_QKROPE, bm, (hipStream_t)stream, &a);
+}
+
 extern "C" int qv_w4a16_gemm_noalloc(const void* x, const void* qweight, const void* scales,
                                      const void* scaled_zeros, const void* bias, void* out, int64_t M,
                                      int64_t N, int64_t K, int dtype, int epilogue, void* stream) {

@@ -102,12 +102,32 @@ __device__ __forceinline__ size_t qw_chunk_u32(int n, int kt, int g, int K) {
 // the LayerScale residual update out = out + gamma * fp16(acc + bias), in
 // place on the residual stream (qv_w4a16_gemm_residual).
 constexpr int QV_EPI_BIAS_RESID = 4;
+// Internal epilogue id of qv_w4a16_gemm_qkrope (fp16 only): the VGGT qkv
+// projection with its per-head q/k LayerNorm and 2-D RoPE (see QkRopeArgs).
+constexpr int QV_EPI_QKROPE = 5;
+
+// Operands of the QV_EPI_QKROPE epilogue.  Output columns [0, qk_cols) are the
+// q heads then the k heads (64 columns each), the rest pass through with the
+// bias; positions are int32 (y, x) per output row, cos/sin fp32 (P, 16).
+struct QkRopeArgs {
+  const int* pos = nullptr;
+  const float* cos_t = nullptr;
+  const float* sin_t = nullptr;
+  const uint16_t* qg = nullptr;
+  const uint16_t* qb = nullptr;
+  const uint16_t* kg = nullptr;
+  const uint16_t* kb = nullptr;
+  int P = 1;
+  int qk_cols = 0;
+  float eps = 0.f;
+};
 
 // Bias / GELU on four consecutive channels n..n+3 (fp32, before the single
 // rounding to the 16-bit output type).
 template <bool BF16, int EPI>
 __device__ __forceinline__ void epilogue_apply4(const uint16_t* __restrict__ bias, float (&r)[4], int n) {
-  if constexpr (EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_BIAS_RESID) {
+  if constexpr (EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_BIAS_RESID ||
+                EPI == QV_EPI_QKROPE) {
     const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
     r[0] += to_f32((uint16_t)(b.x & 0xFFFF), BF16);
     r[1] += to_f32((uint16_t)(b.x >> 16), BF16);
@@ -170,6 +190,7 @@ __device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, cons
 // Streamed (LDS-pipelined, 32x32 MFMA) GEMM, tile bm x 256 with bm in {32, 64, 96, 128}.
 template <bool BF16>
 int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                        const void* gamma, void* out, int M, int N, int K, int epi, int bm, hipStream_t st);
+                        const void* gamma, void* out, int M, int N, int K, int epi, int bm, hipStream_t st,
+                        const QkRopeArgs* qk = nullptr);
 
 }  // namespace qv

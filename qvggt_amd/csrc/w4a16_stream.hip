@@ -31,7 +31,7 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
                            const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
                            const uint16_t* __restrict__ bias, const uint16_t* __restrict__ gamma,
                            uint16_t* __restrict__ out, int M, int N,
-                           int K, int tiles_n) {
+                           int K, int tiles_n, QkRopeArgs qk) {
   constexpr int BM = 32 * MT, BN = 256, NT = 2;
   constexpr int A_BYTES = BM * 128;
   constexpr int STAGE = A_BYTES;
@@ -192,6 +192,101 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
   // layout cost ~3x the output size in HBM write traffic).
   lds_barrier();  // every wave is done reading the pipeline stages
   uint8_t* stg = lds + wave * (BM * EP);
+  bool staged = false;
+  if constexpr (EPI == QV_EPI_QKROPE && !BF16) {
+    // The wave's 64 columns are one head.  For a q or k head, per output row
+    // (token): y = fp16(acc + bias); per-head LayerNorm over the 64 values
+    // (each lane holds 32 of them, the other 32 sit in lane ^ 32), rounded
+    // to fp16; then the 2-D RoPE of rope2d_kernel: columns [0, 32) rotate
+    // with the token's y position, [32, 64) with its x position, and the
+    // pair (d, d + 16) of a half is registers q and q + 2 of one lane.
+    const int nw = n0 + 64 * wave;
+    if (nw < qk.qk_cols) {
+      staged = true;
+      const bool is_k = nw >= (qk.qk_cols >> 1);
+      const uint16_t* gp = is_k ? qk.kg : qk.qg;
+      const uint16_t* bp = is_k ? qk.kb : qk.qb;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = m0 + 32 * i + l32;
+        const int mc = m < M ? m : M - 1;
+        uint32_t yw[NT][4][2];
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int dl = 32 * j + 8 * q + 4 * h;
+            const uint2 bv = *reinterpret_cast<const uint2*>(bias + nw + dl);
+            yw[j][q][0] = pack2<false>(mix_add<0>(bv.x, acc[j][i][4 * q]), mix_add<1>(bv.x, acc[j][i][4 * q + 1]));
+            yw[j][q][1] = pack2<false>(mix_add<0>(bv.y, acc[j][i][4 * q + 2]), mix_add<1>(bv.y, acc[j][i][4 * q + 3]));
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+              sum = mix_add<0>(yw[j][q][w], sum);
+              sum = mix_add<1>(yw[j][q][w], sum);
+            }
+          }
+        float pa, pb;
+        pair32(sum, pa, pb);
+        const float nm = -((pa + pb) * (1.0f / 64.0f));
+        float d[NT][4][4];
+        float s2 = 0.f;
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+              d[j][q][2 * w] = mix_add<0>(yw[j][q][w], nm);
+              d[j][q][2 * w + 1] = mix_add<1>(yw[j][q][w], nm);
+              s2 = s2 + d[j][q][2 * w] * d[j][q][2 * w];
+              s2 = s2 + d[j][q][2 * w + 1] * d[j][q][2 * w + 1];
+            }
+        pair32(s2, pa, pb);
+        const float rs = 1.0f / __builtin_sqrtf((pa + pb) * (1.0f / 64.0f) + qk.eps);
+        const int2 pp = *reinterpret_cast<const int2*>(qk.pos + 2 * mc);
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          int p = j == 0 ? pp.x : pp.y;
+          p = p < 0 ? 0 : (p >= qk.P ? qk.P - 1 : p);
+          uint32_t zw[4][2];   // LayerNorm output of this half, rounded to fp16
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int dl = 32 * j + 8 * q + 4 * h;
+            const uint2 g = *reinterpret_cast<const uint2*>(gp + dl);
+            const uint2 b = *reinterpret_cast<const uint2*>(bp + dl);
+            const uint32_t gw[2] = {g.x, g.y}, bw[2] = {b.x, b.y};
+#pragma unroll
+            for (int w = 0; w < 2; ++w)
+              zw[q][w] = pack2<false>(mix_add<0>(bw[w], mix_mul<0>(d[j][q][2 * w] * rs, gw[w])),
+                                      mix_add<1>(bw[w], mix_mul<1>(d[j][q][2 * w + 1] * rs, gw[w])));
+          }
+#pragma unroll
+          for (int qq = 0; qq < 2; ++qq) {
+            // frequencies 8 qq + 4 h + e (e = 0..3) of this half, shared by the pair (qq, qq + 2)
+            const float4 c4 = *reinterpret_cast<const float4*>(qk.cos_t + p * 16 + 8 * qq + 4 * h);
+            const float4 s4 = *reinterpret_cast<const float4*>(qk.sin_t + p * 16 + 8 * qq + 4 * h);
+            const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+            uint32_t o1[2], o2[2];
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+              const uint32_t a = zw[qq][w], b = zw[qq + 2][w];
+              // first of the pair: a c - b s; second: b c + a s
+              o1[w] = pack2<false>(mix_mul<0>(cs[2 * w], a) - mix_mul<0>(sn[2 * w], b),
+                                   mix_mul<1>(cs[2 * w + 1], a) - mix_mul<1>(sn[2 * w + 1], b));
+              o2[w] = pack2<false>(mix_mul<0>(cs[2 * w], b) + mix_mul<0>(sn[2 * w], a),
+                                   mix_mul<1>(cs[2 * w + 1], b) + mix_mul<1>(sn[2 * w + 1], a));
+            }
+            *reinterpret_cast<uint2*>(stg + stg_off(32 * i + l32, (32 * j + 8 * qq + 4 * h) * 2)) =
+                make_uint2(o1[0], o1[1]);
+            *reinterpret_cast<uint2*>(stg + stg_off(32 * i + l32, (32 * j + 8 * (qq + 2) + 4 * h) * 2)) =
+                make_uint2(o2[0], o2[1]);
+          }
+        }
+      }
+    }
+  }
+  if (!staged) {
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
 #pragma unroll
@@ -208,6 +303,7 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
         *reinterpret_cast<uint2*>(stg + stg_off(32 * i + l32, nl * 2)) = o;
       }
     }
+  }
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
   __builtin_amdgcn_wave_barrier();
@@ -228,12 +324,13 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
 
 template <bool BF16, int MT>
 static void launch_mt(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                      const void* gamma, void* out, int M, int N, int K, int epi, hipStream_t st) {
+                      const void* gamma, void* out, int M, int N, int K, int epi, hipStream_t st,
+                      const QkRopeArgs& qk) {
   const int tiles_m = (M + 32 * MT - 1) / (32 * MT), tiles_n = (N + 255) / 256;
   const dim3 grid(tiles_m * tiles_n), block(256);
 #define QV_ARGS                                                                                \
   (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,             \
-      (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, tiles_n
+      (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, tiles_n, qk
   switch (epi) {
     case QV_EPI_NONE:
       hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_NONE>), grid, block, 0, st, QV_ARGS);
@@ -247,6 +344,9 @@ static void launch_mt(const void* x, const void* qw, const void* s, const void* 
     case QV_EPI_GELU:
       hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_GELU>), grid, block, 0, st, QV_ARGS);
       break;
+    case QV_EPI_QKROPE:
+      if constexpr (!BF16) hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_QKROPE>), grid, block, 0, st, QV_ARGS);
+      break;
     default:
       hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_BIAS_RESID>), grid, block, 0, st, QV_ARGS);
       break;
@@ -256,17 +356,21 @@ static void launch_mt(const void* x, const void* qw, const void* s, const void* 
 
 template <bool BF16>
 int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                        const void* gamma, void* out, int M, int N, int K, int epi, int bm, hipStream_t st) {
-  if (bm == 128) launch_mt<BF16, 4>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st);
-  else if (bm == 96) launch_mt<BF16, 3>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st);
-  else if (bm == 64) launch_mt<BF16, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st);
-  else launch_mt<BF16, 1>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st);
+                        const void* gamma, void* out, int M, int N, int K, int epi, int bm, hipStream_t st,
+                        const QkRopeArgs* qk) {
+  const QkRopeArgs a = qk ? *qk : QkRopeArgs();
+  if (bm == 128) launch_mt<BF16, 4>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  else if (bm == 96) launch_mt<BF16, 3>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  else if (bm == 64) launch_mt<BF16, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  else launch_mt<BF16, 1>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
   return check_launch("w4a16_stream32");
 }
 
 template int launch_w4a16_stream<false>(const void*, const void*, const void*, const void*, const void*,
-                                        const void*, void*, int, int, int, int, int, hipStream_t);
+                                        const void*, void*, int, int, int, int, int, hipStream_t,
+                                        const QkRopeArgs*);
 template int launch_w4a16_stream<true>(const void*, const void*, const void*, const void*, const void*,
-                                       const void*, void*, int, int, int, int, int, hipStream_t);
+                                       const void*, void*, int, int, int, int, int, hipStream_t,
+                                       const QkRopeArgs*);
 
 }  // namespace qv

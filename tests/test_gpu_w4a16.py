@@ -398,3 +398,51 @@ def test_skinny_split_k_bf16(gpu):
     y = E.gemm_forward_cuda_new(x, qw, sct, szt)
     W = O.bf16_bits_to_f32(O.dequantize_bf16_bits(p["qweight"], sc, sz, N, K))
     assert O.rel_err(y.float().cpu().numpy(), O.bf16_bits_to_f32(xb) @ W.T) <= TOL
+
+
+@pytest.mark.parametrize("M", [1374, 2748, 300, 40])
+def test_qkv_qknorm_rope_fused_matches_two_step(gpu, M):
+    """qv_w4a16_gemm_qkrope (the qkv projection with its q/k LayerNorm and 2-D
+    RoPE in the GEMM epilogue) against the two-step path it replaces,
+    qv_w4a16_gemm + qv_qknorm_rope2d, both of which are pinned bit-exact
+    elsewhere.  The v heads are the same GEMM epilogue (bit-identical); the q
+    and k heads sum the LayerNorm statistics in another order, so their
+    LayerNorm outputs may differ by an fp16 rounding step.  M = 40 takes the skinny path, where the
+    entry runs the two steps itself (bit-identical)."""
+    from oracle import rope as R
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd._lib import QV_EPI_BIAS
+    H, K = 16, 1024
+    N = 3 * H * 64
+    p = O.make_w4_problem(M, K, N, seed=M)
+    t = _to_dev(p, gpu)
+    rng = np.random.default_rng(M)
+    bias = torch.from_numpy((rng.standard_normal(N) * 0.5).astype(np.float16)).to(gpu)
+    if M % 1374 == 0:
+        pos = R.vggt_positions(M // 1374)
+    else:
+        pos = rng.integers(0, 38, size=(M, 2)).astype(np.int32)
+    pt = torch.from_numpy(pos).to(gpu)
+    ct, st = E.rope2d_tables(38, device=gpu)
+    qg, qb, kg, kb = (torch.from_numpy(((1 if i % 2 == 0 else 0) + 0.1 * rng.standard_normal(64)).astype(np.float16))
+                      .to(gpu) for i in range(4))
+    fused = E.w4a16_linear_qkrope(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias, pt, ct, st, H,
+                                  qg, qb, kg, kb, eps=1e-6)
+    two = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=bias, epilogue=QV_EPI_BIAS)
+    E.qknorm_rope2d(two, pt, ct, st, H, qg, qb, kg, kb, eps=1e-6)
+    torch.cuda.synchronize()
+    f = fused.view(M, 3, H, 64).cpu().numpy().astype(np.float64)
+    w = two.view(M, 3, H, 64).cpu().numpy().astype(np.float64)
+    assert np.isfinite(f).all()
+    assert np.array_equal(f[:, 2], w[:, 2]), "v heads"
+    if M <= 64:
+        assert np.array_equal(f, w)
+    # The LayerNorm outputs may differ by one fp16 rounding step; the rotation
+    # a c -/+ b s then carries that into its result, which can cancel to far
+    # below the inputs' magnitude, so the bound is in ulps of each head row's
+    # largest value: 2 input steps plus the output rounding.
+    row_max = np.maximum(np.abs(f[:, :2]), np.abs(w[:, :2])).max(axis=-1, keepdims=True)
+    ulp = np.spacing(row_max.astype(np.float16)).astype(np.float64)
+    worst = (np.abs(f[:, :2] - w[:, :2]) / ulp).max()
+    print(f"[qkrope] M={M}: max |fused - two-step| = {worst:.2f} ulp of the head row's max", flush=True)
+    assert worst <= 3.0, f"q/k heads differ by {worst} fp16 ulp of the head row's largest value"
