@@ -20,7 +20,11 @@
 // (h, l), register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the tile.
 // LDS per workgroup: max(3 stages x BM*128, the epilogue staging of 4 x BM x
 // 128 B); BM = 128 -> 64 KB, 2 workgroups/CU.  The epilogue stages each wave's
-// BM x 64 output tile there and writes it back as whole 128-byte rows.
+// BM x 64 output tile there and writes it back as whole 128-byte rows, with
+// non-temporal stores: the output (90 MB for an MLP linear at 43 k tokens)
+// would otherwise evict the weight matrix and the activation rows that the
+// other tiles of the XCD still read from its L2 (fc1 at M = 10992: HBM reads
+// 94.7 -> 43.0 MB per launch).
 #include "w4a16_common.h"
 
 namespace qv {
@@ -317,7 +321,7 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
       if constexpr (EPI == QV_EPI_BIAS_RESID)
         v = resid_update8<BF16>(*reinterpret_cast<const uint4*>(out + (size_t)m * N + n), v,
                                 *reinterpret_cast<const uint4*>(gamma + n));
-      *reinterpret_cast<uint4*>(out + (size_t)m * N + n) = v;
+      st_stream16(out + (size_t)m * N + n, v);
     }
   }
 }

@@ -15,6 +15,8 @@
 // K-slots: k-step s (0..1) of a stage, lane half h: k = 32*s + 16*h + 0..15
 // (16 contiguous bytes = chunk 2s + h) on both operands.  Output: lane (h, l),
 // register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the wave's tile.
+// Outputs are written with non-temporal stores so that they do not evict the
+// operand rows the XCD's other tiles still read from L2.
 #include "common.h"
 
 #pragma clang fp contract(off)
@@ -28,7 +30,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b,
                       const uint16_t* __restrict__ ws, const uint16_t* __restrict__ as,
                       const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
-                      int tiles_n) {
+                      int tiles_n, int gn) {
   constexpr int BM = 32 * MT, BN = 256, NT = 2;
   constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64;
   constexpr int STAGE = A_BYTES + B_BYTES;
@@ -42,9 +44,17 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
+  // Tiles are numbered column group by column group (gn n-tiles wide), row
+  // by row inside a group, and each XCD takes a contiguous range of that
+  // order (xcd_remap): the weight slices of one group stay in the XCD's L2
+  // while it walks down the rows (w8a8_col_group picks gn).
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  const int m0 = (lid / tiles_n) * BM;
-  const int n0 = (lid % tiles_n) * BN;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int g = lid / (tiles_m * gn);
+  const int r = lid - g * tiles_m * gn;
+  const int gw = tiles_n - g * gn < gn ? tiles_n - g * gn : gn;
+  const int m0 = (r / gw) * BM;
+  const int n0 = (g * gn + r % gw) * BN;
   const int KS = K >> 6;
 
   const auto rsA = make_rsrc(a + (size_t)m0 * K, (uint64_t)(M - m0) * K);
@@ -134,7 +144,7 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
           const int m = m0 + 32 * i + l32;
           if (m >= M) continue;
           int4 o = make_int4(acc[j][i][4 * qd], acc[j][i][4 * qd + 1], acc[j][i][4 * qd + 2], acc[j][i][4 * qd + 3]);
-          *reinterpret_cast<int4*>(reinterpret_cast<int32_t*>(out) + (size_t)m * N + n) = o;
+          st_stream16(reinterpret_cast<int32_t*>(out) + (size_t)m * N + n, __builtin_bit_cast(uint4, o));
         }
       }
     }
@@ -199,18 +209,44 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
       const int row = idx >> 3, c = idx & 7;
       const int m = m0 + row, n = n0 + 64 * wave + 8 * c;
       if (m < M && n < N)
-        *reinterpret_cast<uint4*>(o16 + (size_t)m * N + n) = *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16));
+        st_stream16(o16 + (size_t)m * N + n, *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16)));
     }
   }
+}
+
+// Width (in 256-column tiles) of the column groups the tile order walks.  A
+// read model per launch: every column group reads all of A once (its rows
+// are shared by the gn tiles of a row, which run side by side on one XCD),
+// and every XCD reads the weight slices of the groups it works on, once when
+// they fit in about half of its 4 MB L2 next to the A rows in flight, else
+// once per round of its 64 resident tiles.  fc1 of an MLP at 11 k tokens
+// (K = 1024, N = 4096): whole rows read the 4 MB weight matrix ~2.7 times per
+// XCD (~97 MB), groups of 8 tiles read A twice and the weights once per XCD
+// (~38 MB).
+static int w8a8_col_group(long tiles_m, int tiles_n, long M, long K) {
+  const double a_bytes = (double)M * K, slice = 256.0 * K;
+  const double xcd_rounds = (double)tiles_m * tiles_n / (8.0 * 64.0);
+  int best = tiles_n;
+  double best_cost = 0;
+  for (int gn = tiles_n; gn >= 1; --gn) {
+    const int groups = (tiles_n + gn - 1) / gn;
+    const double groups_per_xcd = groups > 8 ? groups / 8.0 : 1.0;
+    const double w_xcd = gn * slice <= 2.0 * 1024 * 1024 ? groups_per_xcd * gn * slice
+                                                         : (xcd_rounds > 1 ? xcd_rounds : 1) * gn * slice;
+    const double cost = a_bytes * groups + 8.0 * w_xcd;
+    if (gn == tiles_n || cost < best_cost) best = gn, best_cost = cost;
+  }
+  return best;
 }
 
 template <int MT, int OUT>
 static void launch(const void* a, const void* b, const void* ws, const void* as, const void* bias, void* out,
                    int M, int N, int K, hipStream_t st) {
   const int tiles_m = (M + 32 * MT - 1) / (32 * MT), tiles_n = (N + 255) / 256;
+  const int gn = w8a8_col_group(tiles_m, tiles_n, M, K);
   hipLaunchKernelGGL((w8a8_gemm_kernel<MT, OUT>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
                      (const int8_t*)a, (const int8_t*)b, (const uint16_t*)ws, (const uint16_t*)as,
-                     (const uint16_t*)bias, out, M, N, K, tiles_n);
+                     (const uint16_t*)bias, out, M, N, K, tiles_n, gn);
 }
 
 static int w8a8_run(const void* a, const void* b, const void* ws, const void* as, const void* bias, void* out,

@@ -63,8 +63,11 @@ def test_invoke_quant_bit_exact(gpu, M, D, dt):
 
 
 # ------------------------------------------------------------------ GEMM
+# (4100, 4112) and (3001, 4624) walk the tiles in column groups of 6 and 5
+# whose last group is narrower (17 and 19 tile columns); (10992, 4096) in two
+# groups of 8; the others in whole rows.
 @pytest.mark.parametrize("M,N,K", [(10992, 4096, 1024), (10992, 1024, 4096), (300, 3072, 1024), (1, 48, 64),
-                                   (37, 272, 192)])
+                                   (37, 272, 192), (4100, 4112, 1024), (3001, 4624, 1024)])
 def test_w8a8_int32_bit_exact(gpu, M, N, K):
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(M * 7 + N)
@@ -75,7 +78,7 @@ def test_w8a8_int32_bit_exact(gpu, M, N, K):
 
 
 @pytest.mark.parametrize("bias", [False, True])
-@pytest.mark.parametrize("M,N,K", [(2748, 4096, 1024), (129, 1024, 4096)])
+@pytest.mark.parametrize("M,N,K", [(2748, 4096, 1024), (129, 1024, 4096), (4100, 4112, 1024)])
 def test_w8a8_gemm_fp16_bit_exact(gpu, M, N, K, bias):
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(M + N + K)
