@@ -6,7 +6,10 @@
 
 #include <map>
 #include <mutex>
+#include <queue>
+#include <tuple>
 #include <utility>
+#include <vector>
 
 namespace qv {
 
@@ -299,9 +302,11 @@ __global__ __launch_bounds__(256) void w4a16_pack_tables_kernel(
 }
 
 // ------------------------------------------------------------- launchers
-// Tile choice (w4_pick_tile): streamed kernel with BM = 128 / 96 / 64 / 32
-// (x 256); two workgroups run per CU (512 slots on 256 CUs).  M <= 64 goes to
-// the skinny kernel, whose grid covers the channels instead of M x N tiles.
+// Kernel choice (w4_pick_tile): M <= 64 goes to the skinny kernel (5), whose
+// grid covers the channels instead of M x N tiles; a grid that the 32-row
+// tile keeps within one tile per CU takes that tile (6); everything else
+// goes to the streamed kernel with the tile plan of w4_stream_plan below.
+// Two workgroups run per CU (512 slots on 256 CUs).
 static int w4_pick_tile(int M, int N, int K) {
   // the skinny kernel addresses the activations with 32-bit buffer offsets
   const bool skinny_ok = M <= 64 && (int64_t)M * K * 2 < ((int64_t)1 << 31);
@@ -326,6 +331,157 @@ static int w4_pick_tile(int M, int N, int K) {
   return best;
 }
 
+// Tile plan of the streamed kernel (w4_stream_plan).  A launch whose last
+// round of tiles leaves slots idle loses up to a tile's time; covering the
+// rows in two ranges, whole rounds of 128- or 96-row tiles and then shorter
+// tiles, lets the short tiles fill the slots that free up first.  The plan
+// is chosen with an event-driven model of the launch: 256 CUs x 2 workgroup
+// slots, workgroups dispatched in grid order to the slot that frees first
+// (simultaneous completions refill the CUs breadth-first), a tile's work
+// = prologue + stages x per-stage time of its height + epilogue per row,
+// and two co-resident tiles each progressing at 0.62 of the rate of a tile
+// alone on its CU.  The constants (microseconds, shader clock ~2.1 GHz) are
+// fitted to 28 timings of single- and two-range launches at M = 1374 ..
+// 43968, K = 1024 / 4096, N = 1024 .. 4096 (rms error ~5 %).  Only the
+// ranking matters; the model is run once per shape and cached.
+namespace {
+constexpr int PLAN_CUS = 256;
+constexpr double PLAN_SHARED_RATE = 0.623;
+
+double w4_tile_us(int mt, int K, bool gelu) {
+  const double per_stage = mt == 4 ? 0.907 : (mt == 3 ? 0.779 : 0.567);
+  return 1.48 + (K / 64) * per_stage + 32 * mt * (gelu ? 0.0482 : 0.0080);
+}
+
+// Finish time of n_a tiles of work w_a followed (in dispatch order) by n_b
+// tiles of work w_b.  Slot s = pass * PLAN_CUS + cu; its CU partner is
+// s +- PLAN_CUS.
+double w4_simulate(int n_a, double w_a, int n_b, double w_b) {
+  struct Slot { double rem = 0, t0 = 0; int ver = 0; bool busy = false; };
+  std::vector<Slot> slot(2 * PLAN_CUS);
+  using Ev = std::pair<double, std::pair<int, int>>;
+  std::priority_queue<Ev, std::vector<Ev>, std::greater<Ev>> pq;
+  const int total = n_a + n_b;
+  int next = 0;
+  double now = 0, end = 0;
+  auto mate = [](int s) { return s < PLAN_CUS ? s + PLAN_CUS : s - PLAN_CUS; };
+  auto rate = [&](int s) { return slot[mate(s)].busy ? PLAN_SHARED_RATE : 1.0; };
+  auto take = [&](int s) {
+    slot[s].busy = next < total;
+    if (slot[s].busy) {
+      slot[s].rem = next < n_a ? w_a : w_b;
+      slot[s].t0 = now;
+      ++next;
+    }
+  };
+  auto push = [&](int s) {
+    if (!slot[s].busy) return;
+    ++slot[s].ver;
+    pq.push({now + slot[s].rem / rate(s), {s, slot[s].ver}});
+  };
+  for (int s = 0; s < 2 * PLAN_CUS; ++s) take(s);
+  for (int s = 0; s < 2 * PLAN_CUS; ++s) push(s);
+  while (!pq.empty()) {
+    const Ev e = pq.top();
+    pq.pop();
+    const int s = e.second.first, o = mate(s);
+    if (!slot[s].busy || e.second.second != slot[s].ver) continue;
+    now = end = e.first;
+    if (slot[o].busy) {  // the partner ran at the shared rate until now
+      slot[o].rem -= (now - slot[o].t0) * rate(o);
+      slot[o].t0 = now;
+    }
+    take(s);
+    push(s);
+    push(o);
+  }
+  return end;
+}
+
+double w4_plan_time(int M, int N, int K, bool gelu, const StreamPlan& p) {
+  const int tn = (N + 255) / 256;
+  const int rows_a = p.mt_b ? p.rows_a : M;
+  const int n_a = (rows_a + 32 * p.mt_a - 1) / (32 * p.mt_a) * tn;
+  const int n_b = p.mt_b ? (M - rows_a + 32 * p.mt_b - 1) / (32 * p.mt_b) * tn : 0;
+  return w4_simulate(n_a, w4_tile_us(p.mt_a, K, gelu), n_b, p.mt_b ? w4_tile_us(p.mt_b, K, gelu) : 0.0);
+}
+
+StreamPlan w4_stream_plan_uncached(int M, int N, int K, bool gelu) {
+  const int tn = (N + 255) / 256;
+  StreamPlan best;
+  double best_t = 1e300;
+  for (int mt : {4, 3, 2}) {
+    StreamPlan p;
+    p.mt_a = mt;
+    const double t = w4_plan_time(M, N, K, gelu, p);
+    if (t < best_t) best_t = t, best = p;
+  }
+  // Past 16 rounds of 128-row tiles the last round is < 7 % of the launch.
+  if ((int64_t)(M + 127) / 128 * tn > 16 * 2 * PLAN_CUS) return best;
+  const double single_t = best_t;
+  const StreamPlan single = best;
+  const int pairs[3][2] = {{4, 3}, {4, 2}, {3, 2}};
+  for (const auto& pr : pairs) {
+    const int bm = 32 * pr[0];
+    const int jmax = (M - 1) / bm;  // rows_a = j * bm < M
+    if (jmax < 1) continue;
+    const int step = jmax > 16 ? jmax / 16 : 1;
+    int best_j = 0;
+    double pair_t = 1e300;
+    auto eval = [&](int j) {
+      StreamPlan p;
+      p.mt_a = pr[0];
+      p.rows_a = j * bm;
+      p.mt_b = pr[1];
+      const double t = w4_plan_time(M, N, K, gelu, p);
+      if (t < pair_t) pair_t = t, best_j = j;
+    };
+    // a coarse scan plus every split whose first range ends within two tile
+    // rows of a whole number of rounds, then the neighbours of the best
+    for (int j = 1; j <= jmax; ++j) {
+      const int r = (int)((int64_t)j * tn % (2 * PLAN_CUS));
+      if (j % step == 0 || r <= 2 * tn || 2 * PLAN_CUS - r <= 2 * tn) eval(j);
+    }
+    const int c = best_j;
+    for (int j = c - step + 1; j < c + step; ++j)
+      if (j >= 1 && j <= jmax && j != c) eval(j);
+    if (pair_t < best_t) {
+      best_t = pair_t;
+      best.mt_a = pr[0];
+      best.rows_a = best_j * bm;
+      best.mt_b = pr[1];
+    }
+  }
+  // keep one tile height unless two ranges are predicted > 2 % faster
+  return best_t < 0.98 * single_t ? best : single;
+}
+
+StreamPlan w4_stream_plan(int M, int N, int K, bool gelu) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, int, bool>, StreamPlan> cache;
+  const auto key = std::make_tuple(M, N, K, gelu);
+  {
+    std::lock_guard<std::mutex> g(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  const StreamPlan p = w4_stream_plan_uncached(M, N, K, gelu);
+  std::lock_guard<std::mutex> g(mu);
+  if (cache.size() >= 4096) cache.clear();
+  cache[key] = p;
+  return p;
+}
+
+StreamPlan w4_plan_for(int tile, int M, int N, int K, int epi) {
+  StreamPlan p;
+  if (tile == 6) {  // a grid of at most one tile per CU: the 32-row tile
+    p.mt_a = 1;
+    return p;
+  }
+  return w4_stream_plan(M, N, K, epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU);
+}
+}  // namespace
+
 // Split-K workspace of the skinny kernel: fp32 partials and one arrival
 // counter per channel block (zero between launches: the finishing split
 // resets it).
@@ -349,18 +505,14 @@ static int launch_skinny(const void* x, const void* qw, const void* s, const voi
 template <bool BF16>
 static int launch_gemm(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                        void* out, int M, int N, int K, int epi, hipStream_t st, const void* gamma = nullptr) {
-  switch (w4_pick_tile(M, N, K)) {
-    case 2: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 96, st);
-    case 3: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 64, st);
-    case 5: {
-      SplitWorkspace ws;
-      const int rc = split_workspace(st, ws);
-      if (rc) return rc;
-      return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st, gamma, ws.part ? &ws : nullptr);
-    }
-    case 6: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 32, st);
-    default: return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, 128, st);
+  const int tile = w4_pick_tile(M, N, K);
+  if (tile == 5) {
+    SplitWorkspace ws;
+    const int rc = split_workspace(st, ws);
+    if (rc) return rc;
+    return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st, gamma, ws.part ? &ws : nullptr);
   }
+  return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, w4_plan_for(tile, M, N, K, epi), st);
 }
 
 // Channel blocks per skinny workgroup: NB = 2 from M = 5 when N >= 4096
@@ -678,9 +830,9 @@ extern "C" int qv_w4a16_gemm_qkrope(const void* x, const void* qweight, const vo
   a.P = (int)table_rows;
   a.qk_cols = (int)(2 * H * 64);
   a.eps = eps;
-  const int bm = tile == 2 ? 96 : (tile == 3 ? 64 : (tile == 6 ? 32 : 128));
   return launch_w4a16_stream<false>(x, qweight, scales, scaled_zeros, bias, nullptr, out, (int)M, (int)N, (int)K,
-                                    QV_EPI_QKROPE, bm, (hipStream_t)stream, &a);
+                                    QV_EPI_QKROPE, w4_plan_for(tile, (int)M, (int)N, (int)K, QV_EPI_QKROPE),
+                                    (hipStream_t)stream, &a);
 }
 
 extern "C" int qv_w4a16_gemm_noalloc(const void* x, const void* qweight, const void* scales,

@@ -187,10 +187,18 @@ __device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, cons
   epilogue_store4<BF16, EPI>(out, bias, v[0], v[1], v[2], v[3], m, n, N);
 }
 
-// Streamed (LDS-pipelined, 32x32 MFMA) GEMM, tile bm x 256 with bm in {32, 64, 96, 128}.
+// Tile plan of one streamed launch: rows [0, rows_a) in (32 mt_a)-row tiles
+// and rows [rows_a, M) in (32 mt_b)-row tiles; mt_b = 0: every row in
+// (32 mt_a)-row tiles.  Pairs (4, 3), (4, 2), (3, 2); rows_a a multiple of
+// 32 mt_a.
+struct StreamPlan {
+  int mt_a = 4, rows_a = 0, mt_b = 0;
+};
+
+// Streamed (LDS-pipelined, 32x32 MFMA) GEMM, tiles (32 mt) x 256.
 template <bool BF16>
 int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                        const void* gamma, void* out, int M, int N, int K, int epi, int bm, hipStream_t st,
-                        const QkRopeArgs* qk = nullptr);
+                        const void* gamma, void* out, int M, int N, int K, int epi, const StreamPlan& plan,
+                        hipStream_t st, const QkRopeArgs* qk = nullptr);
 
 }  // namespace qv

@@ -19,7 +19,10 @@
 // operands (activations: 8 contiguous halves of chunk 4h + s).  Output: lane
 // (h, l), register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the tile.
 // LDS per workgroup: max(3 stages x BM*128, the epilogue staging of 4 x BM x
-// 128 B); BM = 128 -> 64 KB, 2 workgroups/CU.  The epilogue stages each wave's
+// 128 B); BM = 128 -> 64 KB, 2 workgroups/CU.  One launch may cover its rows
+// in two ranges of different tile heights (StreamPlan): whole rounds of the
+// larger tile, then shorter tiles that fill the slots freed first; a tile's
+// results do not depend on its height.  The epilogue stages each wave's
 // BM x 64 output tile there and writes it back as whole 128-byte rows, with
 // non-temporal stores: the output (90 MB for an MLP linear at 43 k tokens)
 // would otherwise evict the weight matrix and the activation rows that the
@@ -30,12 +33,11 @@
 namespace qv {
 
 template <bool BF16, int MT, int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
-                           const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
-                           const uint16_t* __restrict__ bias, const uint16_t* __restrict__ gamma,
-                           uint16_t* __restrict__ out, int M, int N,
-                           int K, int tiles_n, QkRopeArgs qk) {
+__device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uint16_t* __restrict__ x,
+                                            const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scales,
+                                            const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
+                                            const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out, int M,
+                                            int N, int K, int tiles_n, const QkRopeArgs& qk, int lid, int m_base) {
   constexpr int BM = 32 * MT, BN = 256, NT = 2;
   constexpr int A_BYTES = BM * 128;
   constexpr int STAGE = A_BYTES;
@@ -43,15 +45,13 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
   constexpr int A_INSTR = BM / 32;                // 1 KB direct loads per wave for A
   static_assert(A_INSTR < 16, "vmcnt immediate");
   constexpr int EP = 128;  // bytes per staged epilogue row (64 fp16, chunk-swizzled: stg_off)
-  constexpr int LDS_BYTES = NSTAGE * STAGE > 4 * BM * EP ? NSTAGE * STAGE : 4 * BM * EP;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  static_assert(NSTAGE * STAGE <= 4 * BM * EP, "the epilogue staging is the larger LDS user");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int h = lane >> 5, l32 = lane & 31;
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  const int m0 = (lid / tiles_n) * BM;
+  const int m0 = m_base + (lid / tiles_n) * BM;
   const int n0 = (lid % tiles_n) * BN;
   const int K2 = K * 2;
   const int KS = K >> 6;
@@ -326,33 +326,59 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
   }
 }
 
-template <bool BF16, int MT>
+// One launch over two row ranges: blocks [0, n_first) take 32*MT-row tiles of
+// rows [0, m_split), the rest 32*MT2-row tiles of rows [m_split, M) (MT2 = 0:
+// one range).  Each range maps its blocks to tiles on its own (xcd_remap of
+// the block's index within the range).
+template <bool BF16, int MT, int MT2, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
+                           const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+                           const uint16_t* __restrict__ bias, const uint16_t* __restrict__ gamma,
+                           uint16_t* __restrict__ out, int M, int N, int K, int tiles_n, QkRopeArgs qk,
+                           int n_first, int m_split) {
+  constexpr int MTX = MT > MT2 ? MT : MT2;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * 32 * MTX * 128];
+  const int b = blockIdx.x;
+  if (MT2 == 0 || b < n_first) {
+    stream_tile<BF16, MT, EPI>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
+                               xcd_remap(b, MT2 == 0 ? (int)gridDim.x : n_first), 0);
+  } else {
+    stream_tile<BF16, (MT2 > 0 ? MT2 : 1), EPI>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
+                                                xcd_remap(b - n_first, (int)gridDim.x - n_first), m_split);
+  }
+}
+
+template <bool BF16, int MT, int MT2 = 0>
 static void launch_mt(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                       const void* gamma, void* out, int M, int N, int K, int epi, hipStream_t st,
-                      const QkRopeArgs& qk) {
-  const int tiles_m = (M + 32 * MT - 1) / (32 * MT), tiles_n = (N + 255) / 256;
-  const dim3 grid(tiles_m * tiles_n), block(256);
+                      const QkRopeArgs& qk, int m_split = 0) {
+  const int tiles_n = (N + 255) / 256;
+  const int rows1 = MT2 ? m_split : M;
+  const int n_first = (rows1 + 32 * MT - 1) / (32 * MT) * tiles_n;
+  const int n_second = MT2 ? (M - m_split + 32 * MT2 - 1) / (32 * MT2) * tiles_n : 0;
+  const dim3 grid(n_first + n_second), block(256);
 #define QV_ARGS                                                                                \
   (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,             \
-      (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, tiles_n, qk
+      (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, tiles_n, qk, n_first, m_split
   switch (epi) {
     case QV_EPI_NONE:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_NONE>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_NONE>), grid, block, 0, st, QV_ARGS);
       break;
     case QV_EPI_BIAS:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_BIAS>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS>), grid, block, 0, st, QV_ARGS);
       break;
     case QV_EPI_BIAS_GELU:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_BIAS_GELU>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS_GELU>), grid, block, 0, st, QV_ARGS);
       break;
     case QV_EPI_GELU:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_GELU>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_GELU>), grid, block, 0, st, QV_ARGS);
       break;
     case QV_EPI_QKROPE:
-      if constexpr (!BF16) hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_QKROPE>), grid, block, 0, st, QV_ARGS);
+      if constexpr (!BF16) hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_QKROPE>), grid, block, 0, st, QV_ARGS);
       break;
     default:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, QV_EPI_BIAS_RESID>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS_RESID>), grid, block, 0, st, QV_ARGS);
       break;
   }
 #undef QV_ARGS
@@ -360,21 +386,33 @@ static void launch_mt(const void* x, const void* qw, const void* s, const void* 
 
 template <bool BF16>
 int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                        const void* gamma, void* out, int M, int N, int K, int epi, int bm, hipStream_t st,
-                        const QkRopeArgs* qk) {
+                        const void* gamma, void* out, int M, int N, int K, int epi, const StreamPlan& p,
+                        hipStream_t st, const QkRopeArgs* qk) {
   const QkRopeArgs a = qk ? *qk : QkRopeArgs();
-  if (bm == 128) launch_mt<BF16, 4>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
-  else if (bm == 96) launch_mt<BF16, 3>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
-  else if (bm == 64) launch_mt<BF16, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
-  else launch_mt<BF16, 1>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  if (p.mt_b) {
+    QV_CHECK_ARG(p.rows_a > 0 && p.rows_a < M && p.rows_a % (32 * p.mt_a) == 0,
+                 "bad tile plan: %d rows of %d-row tiles for M=%d", p.rows_a, 32 * p.mt_a, M);
+    if (p.mt_a == 4 && p.mt_b == 3) launch_mt<BF16, 4, 3>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a, p.rows_a);
+    else if (p.mt_a == 4 && p.mt_b == 2) launch_mt<BF16, 4, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a, p.rows_a);
+    else if (p.mt_a == 3 && p.mt_b == 2) launch_mt<BF16, 3, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a, p.rows_a);
+    else QV_CHECK_ARG(false, "bad tile plan: tile pair %d/%d", p.mt_a, p.mt_b);
+  } else if (p.mt_a == 4) {
+    launch_mt<BF16, 4>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  } else if (p.mt_a == 3) {
+    launch_mt<BF16, 3>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  } else if (p.mt_a == 2) {
+    launch_mt<BF16, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  } else {
+    launch_mt<BF16, 1>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  }
   return check_launch("w4a16_stream32");
 }
 
 template int launch_w4a16_stream<false>(const void*, const void*, const void*, const void*, const void*,
-                                        const void*, void*, int, int, int, int, int, hipStream_t,
+                                        const void*, void*, int, int, int, int, const StreamPlan&, hipStream_t,
                                         const QkRopeArgs*);
 template int launch_w4a16_stream<true>(const void*, const void*, const void*, const void*, const void*,
-                                       const void*, void*, int, int, int, int, int, hipStream_t,
+                                       const void*, void*, int, int, int, int, const StreamPlan&, hipStream_t,
                                        const QkRopeArgs*);
 
 }  // namespace qv

@@ -446,3 +446,50 @@ def test_qkv_qknorm_rope_fused_matches_two_step(gpu, M):
     worst = (np.abs(f[:, :2] - w[:, :2]) / ulp).max()
     print(f"[qkrope] M={M}: max |fused - two-step| = {worst:.2f} ulp of the head row's max", flush=True)
     assert worst <= 3.0, f"q/k heads differ by {worst} fp16 ulp of the head row's largest value"
+
+
+# Shapes whose launch covers the rows in two ranges of different tile heights
+# (the tile planner picks 96- then 64-row tiles for 2748 x 3072, 128- then
+# 96-row tiles for the others), with the epilogue each runs with in the model.
+@pytest.mark.parametrize("M,N,K,epi_name,dt", [(2748, 3072, 1024, "BIAS", "f16"), (10992, 4096, 1024, "BIAS_GELU", "f16"),
+                                               (5496, 4096, 1024, "BIAS_GELU", "f16"), (10992, 3072, 1024, "BIAS", "f16"),
+                                               (21984, 1024, 4096, "BIAS", "f16"), (10992, 3072, 1024, "BIAS", "bf16")])
+def test_two_range_launch_matches_row_slices(gpu, M, N, K, epi_name, dt):
+    """A tile's results do not depend on its height or on which range of the
+    launch it sits in: the whole launch equals, bit for bit, the same linear
+    run on two row slices (each slice gets a plan of its own), and sampled
+    rows stay within the tolerance of the fp32 dequantised reference."""
+    from scipy.special import erf
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd import _lib
+    epi = getattr(_lib, "QV_EPI_" + epi_name)
+    p = O.make_w4_problem(M, K, N, seed=M + N)
+    bias = (np.random.default_rng(M).standard_normal(N) * 0.1).astype(np.float16)
+    if dt == "bf16":
+        x_bits, sc, sz = _bf16_problem(p)
+        x = torch.from_numpy(x_bits.view(np.int16)).to(gpu).view(torch.bfloat16)
+        scales = torch.from_numpy(sc.view(np.int16)).to(gpu).view(torch.bfloat16)
+        zeros = torch.from_numpy(sz.view(np.int16)).to(gpu).view(torch.bfloat16)
+        b = torch.from_numpy(bias).to(gpu).to(torch.bfloat16)
+    else:
+        t = _to_dev(p, gpu)
+        x, scales, zeros = t["x"], t["scales"], t["scaled_zeros"]
+        b = torch.from_numpy(bias).to(gpu)
+    qw = torch.from_numpy(p["qweight"]).to(gpu)
+    whole = E.w4a16_linear(x, qw, scales, zeros, bias=b, epilogue=epi)
+    cut = 1000
+    parts = torch.cat([E.w4a16_linear(x[:cut], qw, scales, zeros, bias=b, epilogue=epi),
+                       E.w4a16_linear(x[cut:], qw, scales, zeros, bias=b, epilogue=epi)])
+    torch.cuda.synchronize()
+    assert torch.equal(whole, parts)
+    rows = np.random.default_rng(1).choice(M, 256, replace=False)
+    xr = x[torch.from_numpy(rows).to(gpu)].float().cpu().numpy()
+    if dt == "bf16":
+        W = O.bf16_bits_to_f32(O.dequantize_bf16_bits(p["qweight"], sc, sz, N, K))
+    else:
+        W = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K)
+    ref = (O.gemm_ref(xr, W) + b.float().cpu().numpy()).astype(np.float64)
+    if epi_name == "BIAS_GELU":
+        ref = 0.5 * ref * (1.0 + erf(ref / np.sqrt(2.0)))
+    got = whole[torch.from_numpy(rows).to(gpu)].float().cpu().numpy()
+    assert np.isfinite(got).all() and O.rel_err(got, ref) <= TOL
