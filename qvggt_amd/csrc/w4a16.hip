@@ -355,8 +355,15 @@ double w4_tile_us(int mt, int K, bool gelu) {
 
 // Finish time of n_a tiles of work w_a followed (in dispatch order) by n_b
 // tiles of work w_b.  Slot s = pass * PLAN_CUS + cu; its CU partner is
-// s +- PLAN_CUS.
+// s +- PLAN_CUS.  A full round of identical tiles starts on every slot at
+// once and ends at once (w_a at the shared rate), after which the state is
+// the starting one: all but the last full round of the first range are
+// skipped in closed form.
 double w4_simulate(int n_a, double w_a, int n_b, double w_b) {
+  const int slots = 2 * PLAN_CUS;
+  const int skip = n_a / slots > 1 ? n_a / slots - 1 : 0;
+  const double t_skip = skip * (w_a / PLAN_SHARED_RATE);
+  n_a -= skip * slots;
   struct Slot { double rem = 0, t0 = 0; int ver = 0; bool busy = false; };
   std::vector<Slot> slot(2 * PLAN_CUS);
   using Ev = std::pair<double, std::pair<int, int>>;
@@ -395,7 +402,7 @@ double w4_simulate(int n_a, double w_a, int n_b, double w_b) {
     push(s);
     push(o);
   }
-  return end;
+  return t_skip + end;
 }
 
 double w4_plan_time(int M, int N, int K, bool gelu, const StreamPlan& p) {
@@ -421,11 +428,17 @@ StreamPlan w4_stream_plan_uncached(int M, int N, int K, bool gelu) {
   const double single_t = best_t;
   const StreamPlan single = best;
   const int pairs[3][2] = {{4, 3}, {4, 2}, {3, 2}};
+  // The second range fills the last rounds: first ranges that end more than
+  // 2.5 rounds of 128-row tiles before the launch does are not tried.
+  const double rounds128 = (double)((M + 127) / 128) * tn / (2 * PLAN_CUS);
   for (const auto& pr : pairs) {
     const int bm = 32 * pr[0];
     const int jmax = (M - 1) / bm;  // rows_a = j * bm < M
-    if (jmax < 1) continue;
-    const int step = jmax > 16 ? jmax / 16 : 1;
+    const double min_tiles = (rounds128 - 2.5) * 2 * PLAN_CUS;
+    const int jmin = min_tiles > tn ? (int)(min_tiles / tn) : 1;
+    if (jmax < jmin) continue;
+    const int span = jmax - jmin + 1;
+    const int step = span > 16 ? span / 16 : 1;
     int best_j = 0;
     double pair_t = 1e300;
     auto eval = [&](int j) {
@@ -438,13 +451,13 @@ StreamPlan w4_stream_plan_uncached(int M, int N, int K, bool gelu) {
     };
     // a coarse scan plus every split whose first range ends within two tile
     // rows of a whole number of rounds, then the neighbours of the best
-    for (int j = 1; j <= jmax; ++j) {
+    for (int j = jmin; j <= jmax; ++j) {
       const int r = (int)((int64_t)j * tn % (2 * PLAN_CUS));
-      if (j % step == 0 || r <= 2 * tn || 2 * PLAN_CUS - r <= 2 * tn) eval(j);
+      if ((j - jmin) % step == 0 || r <= 2 * tn || 2 * PLAN_CUS - r <= 2 * tn) eval(j);
     }
     const int c = best_j;
     for (int j = c - step + 1; j < c + step; ++j)
-      if (j >= 1 && j <= jmax && j != c) eval(j);
+      if (j >= jmin && j <= jmax && j != c) eval(j);
     if (pair_t < best_t) {
       best_t = pair_t;
       best.mt_a = pr[0];
