@@ -32,29 +32,34 @@
 
 namespace qv {
 
-template <bool BF16, int MT, int EPI>
-__device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uint16_t* __restrict__ x,
-                                            const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scales,
-                                            const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
-                                            const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out, int M,
-                                            int N, int K, int tiles_n, const QkRopeArgs& qk, int lid, int m_base) {
-  constexpr int BM = 32 * MT, BN = 256, NT = 2;
+constexpr int EP = 128;  // bytes per staged epilogue row (64 fp16, chunk-swizzled: stg_off)
+
+// Main loop of one tile over its 64-k stages [k0, k1): acc += the tile's
+// products (acc is not cleared here).  Returns with every load landed.
+template <bool BF16, int MT>
+__device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const uint16_t* __restrict__ x,
+                                                const uint32_t* __restrict__ qw,
+                                                const uint16_t* __restrict__ scales,
+                                                const uint16_t* __restrict__ zeros, int M, int N, int K, int m0,
+                                                int n0, int k0, int k1, f32x16 (&acc)[2][MT]) {
+  constexpr int BM = 32 * MT, NT = 2;
   constexpr int A_BYTES = BM * 128;
   constexpr int STAGE = A_BYTES;
   constexpr int NSTAGE = 3;
   constexpr int A_INSTR = BM / 32;                // 1 KB direct loads per wave for A
   static_assert(A_INSTR < 16, "vmcnt immediate");
-  constexpr int EP = 128;  // bytes per staged epilogue row (64 fp16, chunk-swizzled: stg_off)
   static_assert(NSTAGE * STAGE <= 4 * BM * EP, "the epilogue staging is the larger LDS user");
 
-  const int tid = threadIdx.x;
+  // threadIdx.x through an empty asm: the lane-dependent addresses below are
+  // then computed here, not hoisted out of a caller's loop over tiles and
+  // kept live across it (in a kernel that loops over tiles, that hoisting
+  // made the accumulators spill)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int h = lane >> 5, l32 = lane & 31;
-  const int m0 = m_base + (lid / tiles_n) * BM;
-  const int n0 = (lid % tiles_n) * BN;
   const int K2 = K * 2;
-  const int KS = K >> 6;
 
   const auto rsA = make_rsrc(x + (size_t)m0 * K, (uint64_t)(M - m0) * K2);
   const auto rsB = make_rsrc(qw + (size_t)(n0 >> 2) * (K >> 1), (uint64_t)((N - n0) >> 2) * K2);
@@ -98,14 +103,6 @@ __device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uin
       lds_dma16(rsA, a_voff[(r0 >> 3) & 1], r0 * K2 + ks * 128, base + r0 * 128);
     }
   };
-
-  f32x16 acc[NT][MT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j)
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
   const int fa = (l32 & 7) ^ ((l32 >> 3) & 1);  // fA(32*i + l32) is the same for all i
 
@@ -169,32 +166,51 @@ __device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uin
     __builtin_amdgcn_s_waitcnt(0x0F70 | (A_INSTR + B_INSTR));
     lds_barrier();
   };
-  // B registers alternate between two sets; KS = K / 64 is even (K % 128 == 0)
+  // B registers alternate between two sets (stage i = ks - k0 uses set i & 1
+  // and LDS buffer i % 3); k0 and k1 are even (whole 128-k groups), so every
+  // iteration runs two stages.  Loads past k1 - 1 repeat stage k1 - 1.  (An
+  // odd stage count, with a conditional second half, made the compiler
+  // spill the accumulators in a kernel that loops over tiles.)
   uint4 wq0[NT], wq1[NT];
   uint32_t sv0[NT], zv0[NT], sv1[NT], zv1[NT];
-  issue(0, 0);
-  load_b(0, wq0, sv0, zv0);
-  issue(1, 1);
+  const int last = k1 - 1, nks = k1 - k0;
+  issue(k0, 0);
+  load_b(k0, wq0, sv0, zv0);
+  issue(k0 + 1, 1);
   // lands A(0) wherever the compiler places B(0) relative to A(1)
   __builtin_amdgcn_s_waitcnt(0x0F70 | A_INSTR);
-  for (int ks = 0; ks < KS; ks += 2) {
+  for (int i = 0; i < nks; i += 2) {
+    const int ks = k0 + i;
     top_wait();
     load_b(ks + 1, wq1, sv1, zv1);
     b_wait();
-    issue(ks + 2 < KS ? ks + 2 : KS - 1, (ks + 2) % NSTAGE);
-    compute(ks % NSTAGE, wq0, sv0, zv0);
+    issue(ks + 2 < k1 ? ks + 2 : last, (i + 2) % NSTAGE);
+    compute(i % NSTAGE, wq0, sv0, zv0);
     top_wait();
-    load_b(ks + 2 < KS ? ks + 2 : KS - 1, wq0, sv0, zv0);
+    load_b(ks + 2 < k1 ? ks + 2 : last, wq0, sv0, zv0);
     b_wait();
-    issue(ks + 3 < KS ? ks + 3 : KS - 1, (ks + 3) % NSTAGE);
-    compute((ks + 1) % NSTAGE, wq1, sv1, zv1);
+    issue(ks + 3 < k1 ? ks + 3 : last, (i + 3) % NSTAGE);
+    compute((i + 1) % NSTAGE, wq1, sv1, zv1);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the repeated loads may not land during the epilogue
+}
 
-  // ---- epilogue: the wave's BM x 64 output tile goes through LDS so that the
-  // global stores are whole 128-byte rows (direct 8-byte stores from the MFMA
-  // layout cost ~3x the output size in HBM write traffic).
-  lds_barrier();  // every wave is done reading the pipeline stages
+// Epilogue of one tile: the wave's BM x 64 output tile goes through LDS so
+// that the global stores are whole 128-byte rows (direct 8-byte stores from
+// the MFMA layout cost ~3x the output size in HBM write traffic).  Starts
+// with a workgroup barrier (every wave is done reading the pipeline stages).
+template <bool BF16, int MT, int EPI>
+__device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const uint16_t* __restrict__ bias,
+                                                const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out,
+                                                int M, int N, const QkRopeArgs& qk, int m0, int n0,
+                                                const f32x16 (&acc)[2][MT]) {
+  constexpr int BM = 32 * MT, NT = 2;
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));  // as in stream_mainloop
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+  lds_barrier();
   uint8_t* stg = lds + wave * (BM * EP);
   bool staged = false;
   if constexpr (EPI == QV_EPI_QKROPE && !BF16) {
@@ -324,6 +340,26 @@ __device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uin
       st_stream16(out + (size_t)m * N + n, v);
     }
   }
+}
+
+// One whole tile: logical tile lid of the rows from m_base.
+template <bool BF16, int MT, int EPI>
+__device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uint16_t* __restrict__ x,
+                                            const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scales,
+                                            const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
+                                            const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out, int M,
+                                            int N, int K, int tiles_n, const QkRopeArgs& qk, int lid, int m_base) {
+  const int m0 = m_base + (lid / tiles_n) * (32 * MT);
+  const int n0 = (lid % tiles_n) * 256;
+  f32x16 acc[2][MT];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+  stream_mainloop<BF16, MT>(lds, x, qw, scales, zeros, M, N, K, m0, n0, 0, K >> 6, acc);
+  stream_epilogue<BF16, MT, EPI>(lds, bias, gamma, out, M, N, qk, m0, n0, acc);
 }
 
 // One launch over two row ranges: blocks [0, n_first) take 32*MT-row tiles of
