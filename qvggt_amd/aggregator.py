@@ -24,8 +24,8 @@ reference's tanh gelu_and_quant).  LayerNorm eps, depth and the RoPE base
 come from ``AggregatorConfig`` (a checkpoint's config.json); its defaults are
 the benchmark configuration's LayerNorm(1024, eps 1e-6) and 24 + 24 blocks.
 
-Every hot op runs on libqvggt_hip.so; only the DINOv2 fp16 linears (plain
-GEMMs: hipBLASLt through torch), its GELU, the patch convolution and the
+Every hot op runs on libqvggt_hip.so; only the DINOv2 fp16 linears and the
+patch projection (plain GEMMs: hipBLASLt through torch), its GELU and the
 LayerScale residual updates use torch.
 """
 from __future__ import annotations
@@ -362,9 +362,25 @@ class DinoPatchEmbed(nn.Module):
         self.norm = nn.LayerNorm(DIM, eps=eps, **kw)
 
     @torch.no_grad()
+    def project(self, images: torch.Tensor) -> torch.Tensor:
+        """patch_embed.proj (a 14x14, stride-14 nn.Conv2d) of (S, 3, 518, 518)
+        images as (S, 1369, D) tokens.  The convolution is a GEMM over the
+        non-overlapping patches: each patch unfolds to its (channel, y, x)
+        vector -- the order of the flattened conv weight (D, 3, 14, 14) -- and
+        is multiplied in one addmm (M = S * 1369, K = 588, N = 1024,
+        hipBLASLt), so no convolution solver is searched or picked per shape
+        (in a benchmark trace MIOpen's naive direct kernel took 25.6 ms per
+        call on average, most of it on the first calls)."""
+        S = images.shape[0]
+        proj = self.patch_embed.proj
+        patches = (images.reshape(S, 3, GRID, PATCH, GRID, PATCH).permute(0, 2, 4, 1, 3, 5)
+                   .reshape(S * GRID * GRID, 3 * PATCH * PATCH))
+        return torch.addmm(proj.bias, patches, proj.weight.reshape(DIM, -1).t()).view(S, GRID * GRID, DIM)
+
+    @torch.no_grad()
     def forward(self, images: torch.Tensor, ws: dict) -> torch.Tensor:
         S = images.shape[0]
-        p = self.patch_embed.proj(images).flatten(2).transpose(1, 2)          # (S, 1369, D)
+        p = self.project(images)                                             # (S, 1369, D)
         x = torch.empty(S, TOKENS, DIM, dtype=torch.float16, device=images.device)
         x[:, :1] = self.cls_token + self.pos_embed[:, :1]
         x[:, 1:SPECIALS] = self.register_tokens

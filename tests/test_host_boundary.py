@@ -153,3 +153,20 @@ def test_from_linear_recovers_integer_weights():
     # init_only returns zero buffers of the right shapes (loader.py:450)
     e = WQLinear.from_linear(lin, 4, 128, init_only=True)
     assert e.qweight.shape == q.qweight.shape and not e.qweight.any()
+
+
+def test_patch_projection_equals_the_convolution():
+    """DinoPatchEmbed.project (patch unfold + one GEMM) is the 14x14 stride-14
+    nn.Conv2d it replaces, on the same parameters (float64 on the CPU)."""
+    from qvggt_amd import aggregator as AG
+    torch.manual_seed(0)
+    pe = AG.DinoPatchEmbed(torch.device("cpu"), depth=0).double()
+    with torch.no_grad():
+        pe.patch_embed.proj.weight.normal_()
+        pe.patch_embed.proj.bias.normal_()
+    img = torch.rand(2, 3, AG.IMG, AG.IMG, dtype=torch.float64)
+    with torch.no_grad():
+        ref = pe.patch_embed.proj(img).flatten(2).transpose(1, 2)
+    got = pe.project(img)
+    assert got.shape == (2, AG.GRID * AG.GRID, AG.DIM)
+    assert torch.allclose(got, ref, rtol=1e-12, atol=1e-10)
