@@ -415,6 +415,26 @@ double w4_plan_time(int M, int N, int K, bool gelu, const StreamPlan& p) {
 
 StreamPlan w4_stream_plan_uncached(int M, int N, int K, bool gelu) {
   const int tn = (N + 255) / 256;
+  // Long K (>= 4096, 64 stages) in at most one round of slots: one 128-row
+  // tile per CU first, the remaining rows in 64-row tiles.  Measured at
+  // K = 4096: two co-resident tiles of one height each progress at only
+  // 0.48 (128-row) to 0.57 (64-row) of their solo rate -- they start
+  // together and stall together -- while a 128-row tile beside a 64-row one
+  // progresses at ~0.65, so this plan beats every single-height one (fc2 of
+  // the MLP at M = 10992: 87.7-89.9 us against 91.1-99.8 us for 96-row
+  // tiles, two boxes).  The event model below assumes one co-residence rate
+  // and misses this.
+  if (K >= 4096) {
+    const int rows_a = PLAN_CUS / tn * 128;
+    const int64_t tiles = (int64_t)rows_a / 128 * tn + (int64_t)(M - rows_a + 63) / 64 * tn;
+    if (rows_a > 0 && rows_a < M && tiles <= 2 * PLAN_CUS) {
+      StreamPlan p;
+      p.mt_a = 4;
+      p.rows_a = rows_a;
+      p.mt_b = 2;
+      return p;
+    }
+  }
   StreamPlan best;
   double best_t = 1e300;
   for (int mt : {4, 3, 2}) {
