@@ -298,18 +298,15 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
           base[qb] = m_use[qb];
         }
         l_run[qb] += t;
-      }
-      // ---- O^T += V^T P^T: each V^T fragment (16 contiguous bytes) feeds both query blocks
+        // ---- O^T += V^T P^T for this query block (each V^T fragment feeds
+        // both blocks), issued before the next block's softmax so these
+        // MFMAs run under its VALU work
   #pragma unroll
-      for (int db = 0; db < 2; ++db) {
+        for (int db = 0; db < 2; ++db)
   #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const uint4 vf = vfr[db][st];
-  #pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-            o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
+          for (int st = 0; st < 4; ++st)
+            o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vfr[db][st]),
                                                               __builtin_bit_cast(f16x8, pf[qb][st]), o[qb][db], 0, 0, 0);
-        }
       }
     }
     if (more) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next K and V tiles landed
