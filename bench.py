@@ -332,7 +332,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
+              "the path is measured on one GPU's share of the work, and sharding across GPUs "
+              "is not implemented", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
