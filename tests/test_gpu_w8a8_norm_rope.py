@@ -63,11 +63,13 @@ def test_invoke_quant_bit_exact(gpu, M, D, dt):
 
 
 # ------------------------------------------------------------------ GEMM
-# (4100, 4112) and (3001, 4624) walk the tiles in column groups of 6 and 5
+# K = 64, 128, 192 and 256 cover one to four 64-k stages (the pipeline's
+# prologue and last-stage paths); (4100, 4112) and (3001, 4624) walk the tiles in column groups of 6 and 5
 # whose last group is narrower (17 and 19 tile columns); (10992, 4096) in two
 # groups of 8; the others in whole rows.
 @pytest.mark.parametrize("M,N,K", [(10992, 4096, 1024), (10992, 1024, 4096), (300, 3072, 1024), (1, 48, 64),
-                                   (37, 272, 192), (4100, 4112, 1024), (3001, 4624, 1024)])
+                                   (50, 64, 128), (37, 272, 192), (200, 512, 256), (4100, 4112, 1024),
+                                   (3001, 4624, 1024)])
 def test_w8a8_int32_bit_exact(gpu, M, N, K):
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(M * 7 + N)
