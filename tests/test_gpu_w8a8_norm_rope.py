@@ -100,7 +100,7 @@ def test_w8a8_gemm_fp16_bit_exact(gpu, M, N, K, bias):
 
 
 # ------------------------------------------------------- LN + quant
-@pytest.mark.parametrize("M,D,dt", [(10992, 1024, "f16"), (33, 4096, "f16"), (7, 1000, "f16"),
+@pytest.mark.parametrize("M,D,dt", [(10992, 1024, "f16"), (33, 4096, "f16"), (7, 1000, "f16"), (1001, 2048, "f16"), (18, 512, "f16"),
                                     (1374, 1024, "bf16"), (65, 4096, "bf16"), (300, 1024, "f32"), (9, 2048, "f32")])
 def test_rms_norm_general_per_token_bit_exact(gpu, M, D, dt):
     """layernorm.cu:166-190 dispatches float, half and bfloat16."""
