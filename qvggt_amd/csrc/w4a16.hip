@@ -195,10 +195,19 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
   if (tid == 0) __hip_atomic_exchange(cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (int e = tid; e < M * 16 * NB; e += blockDim.x) {
     const int m = e / (16 * NB), cn = e % (16 * NB), j = cn >> 4, c = cn & 15;
+    // the partials of up to four splits are loaded together (one L2 round
+    // trip, not one per split), then added in split order
     float v = 0.f;
-    for (int k2 = 0; k2 < SK; ++k2) {
-      const float t = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsP, slot(k2, j, m, c), 0, 16));
-      v = k2 == 0 ? t : v + t;
+    for (int k0 = 0; k0 < SK; k0 += 4) {
+      float t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        t[u] = k0 + u < SK ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                           rsP, slot(k0 + u, j, m, c), 0, 16))
+                           : 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (k0 + u < SK) v = k0 + u == 0 ? t[u] : v + t[u];
     }
     epilogue(v, m, n0 + cn);
   }
