@@ -41,15 +41,14 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def blas_threads() -> int:
-    try:
-        from threadpoolctl import threadpool_info
-        n = [i.get("num_threads", 0) for i in threadpool_info() if i.get("user_api") == "blas"]
-        if n:
-            return int(max(n))
-    except Exception:
-        pass
-    return os.cpu_count() or 1
+def cpu_threads() -> int:
+    """Host threads the CPU leg uses: torch's intra-op pool, which follows
+    OMP_NUM_THREADS (the GPU box's share of host cores) and else
+    os.cpu_count()."""
+    import torch
+    n = os.environ.get("OMP_NUM_THREADS")
+    torch.set_num_threads(int(n) if n and n.isdigit() and int(n) > 0 else (os.cpu_count() or 1))
+    return torch.get_num_threads()
 
 
 def synthetic_w4(M: int, K: int, N: int, seed: int, dev, group: int = 128):
@@ -75,39 +74,129 @@ def synthetic_w4(M: int, K: int, N: int, seed: int, dev, group: int = 128):
     return to(x), to(qw), to(scales), to(szeros)
 
 
-def cpu_baseline_mlp(x, w1, b1, w2, b2, y, M_sample: int = 2748, reps: int = 5):
-    """CPU leg: the oracle (numpy dequantisation + fp32 matmul + erf-GELU) of
-    fc1 -> GELU -> fc2 on the first M_sample tokens of the benchmark's own
-    inputs (two frames, about 10 s of host work), timed on the host.  Also the
-    checker: the GPU's timed output y on those tokens is compared with it.
-    Returns (baseline dict, max|y - y_ref| / max|y_ref|)."""
-    import numpy as np
-    from math import sqrt
-
-    from oracle import awq as O
-    from scipy.special import erf
-
-    xs = x[:M_sample].cpu().numpy()
-    t1 = [t.cpu().numpy() for t in w1]
-    t2 = [t.cpu().numpy() for t in w2]
-    bb1, bb2 = b1.float().cpu().numpy(), b2.float().cpu().numpy()
-    H, D = t1[0].shape[0] * 4, t1[0].shape[1]
+def _median_time(fn, reps: int):
+    """Median wall time of fn() over reps runs after one warm-up run."""
     times = []
     for _ in range(reps + 1):
         t0 = time.perf_counter()
-        W1 = O.dequantize(t1[0], t1[1], t1[2], H, D).astype(np.float32)
-        W2 = O.dequantize(t2[0], t2[1], t2[2], D, H).astype(np.float32)
-        h = xs.astype(np.float32) @ W1.T + bb1
-        h = 0.5 * h * (1.0 + erf(h / sqrt(2.0)))
-        yr = h.astype(np.float16).astype(np.float32) @ W2.T + bb2
+        fn()
         times.append(time.perf_counter() - t0)
-    t = sorted(times[1:])[len(times[1:]) // 2]
+    t = sorted(times[1:])
+    return t[len(t) // 2]
+
+
+def cpu_baseline_mlp(x, w1, b1, w2, b2, y, M_sample: int = 2748, reps: int = 5):
+    """CPU leg: the reference's semantics on the host
+    for fc1 -> GELU -> fc2 on the first M_sample tokens of the benchmark's own
+    inputs (two frames), timed as dequantisation alone (the oracle's numpy
+    w = q * s + sz of both weight matrices), the fp32 matmuls + erf-GELU alone
+    (torch on the dequantised weights), and both together; median of ``reps``
+    after one warm-up, on ``cpu_threads()`` threads.  Also the checker: the
+    GPU's timed output y on those tokens is compared with it.
+    Returns (baseline dict, max|y - y_ref| / max|y_ref|)."""
+    import numpy as np
+    import torch
+
+    from oracle import awq as O
+
+    threads = cpu_threads()
+    xs = torch.from_numpy(x[:M_sample].cpu().numpy().astype(np.float32))
+    t1 = [t.cpu().numpy() for t in w1]
+    t2 = [t.cpu().numpy() for t in w2]
+    bb1, bb2 = b1.float().cpu(), b2.float().cpu()
+    H, D = t1[0].shape[0] * 4, t1[0].shape[1]
+
+    def dequant():
+        return (torch.from_numpy(O.dequantize(t1[0], t1[1], t1[2], H, D).astype(np.float32)),
+                torch.from_numpy(O.dequantize(t2[0], t2[1], t2[2], D, H).astype(np.float32)))
+
+    W1, W2 = dequant()
+
+    def matmul(W1=W1, W2=W2):
+        h = torch.nn.functional.gelu(torch.addmm(bb1, xs, W1.t()))
+        return torch.addmm(bb2, h.half().float(), W2.t())
+
+    t_dq = _median_time(dequant, reps)
+    t_mm = _median_time(matmul, reps)
+    t_both = _median_time(lambda: matmul(*dequant()), reps)
+    yr = matmul().numpy()
     flops = 2 * 2 * M_sample * D * H
     err = O.rel_err(y[:M_sample].float().cpu().numpy(), yr)
-    return dict(value=flops / t / 1e12, unit="TFLOP/s", cores=blas_threads(), kind="port",
+    return dict(value=flops / t_both / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                dequant_s=round(t_dq, 4), matmul_s=round(t_mm, 4), both_s=round(t_both, 4),
                 sample=f"{M_sample // 1374} frames (M={M_sample}) of the benchmark's MLP pair: oracle numpy "
-                       f"dequant + fp32 matmul + erf-GELU, median of {reps} after 1 warm-up, {t:.3f} s each; "
-                       f"CPU: {cpu_model()}"), err
+                       f"dequant of both weight matrices {t_dq:.3f} s, torch fp32 matmuls + erf-GELU {t_mm:.3f} s, "
+                       f"both {t_both:.3f} s (median of {reps} after 1 warm-up) on {threads} threads "
+                       f"(os.cpu_count() = {os.cpu_count()}); CPU: {cpu_model()}"), err
+
+
+def cpu_block_extrapolation(reps: int = 3):
+    """CPU leg for BASELINE configs 3-5: one W4A16 AA
+    block on the host in the reference's semantics (numpy dequantisation of
+    its four linears, torch fp32 LayerNorm / matmuls / SDPA / GELU; q/k-norm
+    and RoPE left out, under 1 % of the work), timed as a frame block at
+    S = 8 (whole) and a global block at S = 32 (linears whole, attention on a
+    1/16 sample of the query rows, scaled up), then extrapolated to the S = 32
+    aggregator: 24 frame + 24 global blocks + 24 DINOv2 blocks (costed as
+    frame blocks without dequantisation).  Labelled as extrapolated."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from oracle import awq as O
+
+    threads = cpu_threads()
+    g = torch.Generator().manual_seed(0)
+    lin = {}
+    for name, (K, N) in (("qkv", (1024, 3072)), ("proj", (1024, 1024)), ("fc1", (1024, 4096)),
+                         ("fc2", (4096, 1024))):
+        _, qw, sc, sz = synthetic_w4(0, K, N, seed=len(name), dev="cpu")
+        lin[name] = (qw.numpy(), sc.numpy(), sz.numpy(), N, K)
+
+    def dequant_all():
+        return {k: torch.from_numpy(O.dequantize(v[0], v[1], v[2], v[3], v[4]).astype(np.float32))
+                for k, v in lin.items()}
+
+    W = dequant_all()
+
+    def block(x, seq, q_frac=1):
+        M = x.shape[0]
+        h = F.layer_norm(x, (1024,))
+        qkv = (h @ W["qkv"].t()).view(M, 3, 16, 64)
+        B = M // seq
+        q = qkv[:, 0].reshape(B, seq, 16, 64).transpose(1, 2)
+        k = qkv[:, 1].reshape(B, seq, 16, 64).transpose(1, 2)
+        v = qkv[:, 2].reshape(B, seq, 16, 64).transpose(1, 2)
+        if q_frac > 1:
+            q = q[:, :, :: q_frac]
+        a = F.scaled_dot_product_attention(q, k, v)
+        a = a.transpose(1, 2).reshape(-1, 1024)
+        if q_frac > 1:                      # the sampled rows stand in for all rows below
+            a = a.repeat(q_frac, 1)[:M]
+        x = x + 0.01 * (a @ W["proj"].t())
+        f = F.gelu(F.layer_norm(x, (1024,)) @ W["fc1"].t())
+        return x + 0.01 * (f @ W["fc2"].t())
+
+    t_dq = _median_time(dequant_all, reps)
+    x8 = torch.randn(8 * 1374, 1024, generator=g)
+    t_frame8 = _median_time(lambda: block(x8, 1374), reps)
+    M = 32 * 1374
+    x32 = torch.randn(M, 1024, generator=g)
+    q_frac = 16
+    qs = x32.view(1, M, 16, 64).transpose(1, 2)
+    t_att_sample = _median_time(lambda: F.scaled_dot_product_attention(qs[:, :, ::q_frac], qs, qs), 1)
+    # the sampled block already holds one 1/q_frac share of the attention
+    t_glob32 = _median_time(lambda: block(x32, M, q_frac), 1) + (q_frac - 1) * t_att_sample
+    frame32 = 4 * t_frame8            # four S = 8 frame blocks' worth of linears and attention
+    dino32 = 4 * t_frame8             # the same shapes, fp16 weights (no dequantisation)
+    agg = 24 * (frame32 + t_dq + t_glob32 + t_dq + dino32)
+    return {"kind": "port", "cores": threads, "extrapolated": True,
+            "dequant_block_s": round(t_dq, 4), "frame_block_S8_s": round(t_frame8 + t_dq, 3),
+            "global_block_S32_s": round(t_glob32 + t_dq, 3), "aggregator_S32_s": round(agg, 1),
+            "aggregator_frames_per_s": round(32 / agg, 5),
+            "method": f"torch fp32 on {threads} threads (os.cpu_count() = {os.cpu_count()}), numpy dequant; "
+                      f"global attention timed on 1/{q_frac} of the query rows and scaled; aggregator = 24 x "
+                      f"(frame S=32 + global S=32 + DINOv2 block) from these timings; CPU: {cpu_model()}"}
 
 
 def aggregator_fps(dev, S: int = 32, reps: int = 3, w8a8: bool = False):
@@ -143,8 +232,9 @@ def aggregator_fps(dev, S: int = 32, reps: int = 3, w8a8: bool = False):
 
 def _time_graph(fn, calls: int, reps: int = 3):
     """Capture `calls` invocations of fn(i) in one HIP graph, replay, return us per call.
-    The graph is captured on the stream that ran the warm-up calls, so the ops'
-    per-stream split-K workspaces already exist when capture starts."""
+    The warm-up calls run on the capture stream first (tile plans are made on
+    a shape's first call, outside the graph); nothing else runs while the
+    graph replays."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -168,10 +258,21 @@ def _time_graph(fn, calls: int, reps: int = 3):
     return e0.elapsed_time(e1) * 1e3 / (reps * calls)
 
 
+def _hbm(fn, calls: int, nb: int, nbytes: float):
+    """An HBM-bound kernel timed cold (call i touches buffer set i % nb, the
+    sets together beyond the 256 MiB Infinity Cache) and warm (every call on
+    set 0, which the cache can hold), both replayed from a HIP graph."""
+    cold = _time_graph(lambda i: fn(i % nb), calls)
+    warm = _time_graph(lambda i: fn(0), calls)
+    return {"us": round(cold, 1), "GB/s": round(nbytes / cold / 1e3, 1),
+            "us_warm": round(warm, 1), "GB/s_warm": round(nbytes / warm / 1e3, 1)}
+
+
 def kernel_suite(dev):
-    """Per-kernel throughput at the benchmark shapes, HBM-bound kernels cold
-    (every call touches a different buffer set; the sets span >= 1 GiB, beyond
-    the 256 MiB Infinity Cache), launches replayed from a HIP graph."""
+    """Per-kernel throughput at the benchmark shapes, launches replayed from a
+    HIP graph; HBM-bound kernels cold (every call touches a different buffer
+    set; the sets span >= 1 GiB, beyond the 256 MiB Infinity Cache) and warm
+    (one buffer set, reused)."""
     import numpy as np
     import torch
 
@@ -207,15 +308,22 @@ def kernel_suite(dev):
     xs = [torch.randn(M, D, **f16) for _ in range(nb)]
     ys = [torch.empty(M, D, **f16) for _ in range(nb)]
     g, b = torch.ones(D, **f16), torch.zeros(D, **f16)
-    us = _time_graph(lambda i: E.layer_norm(xs[i % nb], g, b, 1e-6, out=ys[i % nb]), 12)
-    r["layernorm_S32"] = {"us": round(us, 1), "GB/s": round(4 * M * D / us / 1e3, 1)}
+    r["layernorm_S32"] = _hbm(lambda i: E.layer_norm(xs[i], g, b, 1e-6, out=ys[i]), 12, nb, 4 * M * D)
+    # T5 RMSNorm (layernorm_forward_cuda), same rows
+    r["rmsnorm_S32"] = _hbm(lambda i: E.layernorm_forward_cuda(xs[i].view(32, 1374, D), g, ys[i].view(32, 1374, D),
+                                                               1e-6), 12, nb, 4 * M * D)
     q8 = [torch.empty(M, D, dtype=torch.int8, device=dev) for _ in range(nb)]
     sc = [torch.empty(M, **f16) for _ in range(nb)]
-    us = _time_graph(lambda i: E.invoke_quant(q8[i % nb], xs[i % nb], sc[i % nb]), 12)
-    r["quant_S32"] = {"us": round(us, 1), "GB/s": round((3 * M * D + 2 * M) / us / 1e3, 1)}
-    us = _time_graph(lambda i: E.rms_norm_general(q8[i % nb], xs[i % nb], g, b, sc[i % nb], 1e-6, True), 12)
-    r["layernorm_quant_S32"] = {"us": round(us, 1), "GB/s": round((3 * M * D + 2 * M) / us / 1e3, 1)}
-    del ys, q8
+    r["quant_S32"] = _hbm(lambda i: E.invoke_quant(q8[i], xs[i], sc[i]), 12, nb, 3 * M * D + 2 * M)
+    r["layernorm_quant_S32"] = _hbm(lambda i: E.rms_norm_general(q8[i], xs[i], g, b, sc[i], 1e-6, True), 12, nb,
+                                    3 * M * D + 2 * M)
+    # fused_rope_with_pos on the S = 32 q rows: x (s=43968, b=1, h=16, d=64), fp32
+    # angles (1, s, 64); reads x and the angles, writes the output
+    fr = [torch.rand(1, M, 64, device=dev) * 40 - 20 for _ in range(4)]
+    xr4 = [x.view(M, 1, 16, 64) for x in xs[:4]]
+    r["rope_with_pos_S32"] = _hbm(lambda i: E.fused_rope_with_pos_forward_func(xr4[i], fr[i], False), 8, 4,
+                                  4 * M * D + 4 * M * 64)
+    del ys, q8, fr, xr4
     # W8A8 MLP hidden: GELU + per-token quant at M = 10992, D = 4096 (reads x,
     # writes int8 + the fp16 GELU copy + scales), 4 rotating sets of 450 MB
     Mh, Dh = 8 * 1374, 4096
@@ -223,19 +331,18 @@ def kernel_suite(dev):
     hq = [torch.empty(Mh, Dh, dtype=torch.int8, device=dev) for _ in range(4)]
     ht = [torch.empty(Mh, Dh, **f16) for _ in range(4)]
     hs = torch.empty(Mh, **f16)
-    us = _time_graph(lambda i: E.gelu_and_quant(hq[i % 4], hx[i % 4], hs, ht[i % 4]), 8)
-    r["gelu_quant_M10992x4096"] = {"us": round(us, 1), "GB/s": round((5 * Mh * Dh + 2 * Mh) / us / 1e3, 1)}
+    r["gelu_quant_M10992x4096"] = _hbm(lambda i: E.gelu_and_quant(hq[i], hx[i], hs, ht[i]), 8, 4,
+                                       5 * Mh * Dh + 2 * Mh)
     del hx, hq, ht
     qkv = [torch.randn(M, 3 * D, **f16) for _ in range(4)]    # 4 x 270 MB
     pos = torch.from_numpy(np.tile(np.array([[0, 0]] * 5 + [[i // 37 + 1, i % 37 + 1] for i in range(1369)],
                                              np.int32), (32, 1))).to(dev)
     ct, st = E.rope2d_tables(38, device=dev)
-    us = _time_graph(lambda i: E.rope2d(qkv[i % 4], pos, ct, st, 16, out=qkv[i % 4]), 8)
-    r["rope2d_S32"] = {"us": round(us, 1), "GB/s": round(8 * M * D / us / 1e3, 1)}
+    r["rope2d_S32"] = _hbm(lambda i: E.rope2d(qkv[i], pos, ct, st, 16, out=qkv[i]), 8, 4, 8 * M * D)
     gq = torch.ones(64, **f16)
     bq = torch.zeros(64, **f16)
-    us = _time_graph(lambda i: E.qknorm_rope2d(qkv[i % 4], pos, ct, st, 16, gq, bq, gq, bq), 8)
-    r["qknorm_rope2d_S32"] = {"us": round(us, 1), "GB/s": round(8 * M * D / us / 1e3, 1)}
+    r["qknorm_rope2d_S32"] = _hbm(lambda i: E.qknorm_rope2d(qkv[i], pos, ct, st, 16, gq, bq, gq, bq), 8, 4,
+                                  8 * M * D)
     del qkv, xs
     # skinny M (the GEMV entry): aggregator qkv 1024 -> 3072 and the camera-head
     # fc1 / fc2 shapes, weights cold (rotating sets of ~1 GiB)
@@ -416,6 +523,8 @@ def main():
         cpu, err = cpu_baseline_mlp(x, w1, b1, w2, b2, y)
         log(f"[bench] cpu baseline: {cpu['value']:.4f} TFLOP/s ({cpu['sample']})")
         log(f"[bench] timed output vs oracle on the CPU sample: rel err {err:.3e}")
+        cpu["blocks"] = cpu_block_extrapolation()
+        log(f"[bench] cpu blocks (extrapolated): {cpu['blocks']}")
     traffic, traffic_src = profiled_traffic()
 
     result = {

@@ -124,10 +124,14 @@ int qv_w4a16_gemm_qkrope(const void* x, const void* qweight, const void* scales,
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The skinny path's
  * split-K partials and counters live in a fixed file-scope device array of
- * 8 MiB + 16 KiB per GPU, held until the process ends; N <= 65536 (larger N
- * is refused with QV_EINVAL).  The first call on a device resolves the
- * array's address, so make it outside stream capture.  All calls on one GPU
- * share the array: calls that overlap (concurrent streams or threads) race.
+ * 8 MiB + 16 KiB per GPU, held until the process ends.  A split that would
+ * not fit there (more than 4096 channel blocks or 2 Mi partial values) runs
+ * unsplit, exactly as qv_w4a16_gemm plans it, so no shape is refused for the
+ * array's size.  The first split-K call on a device resolves the array's
+ * address and clears its counters (a kernel, then a wait), so make it outside
+ * stream capture (under capture it fails with QV_EINVAL); after that, calls
+ * may be captured.  All calls on one GPU share the array: calls that overlap
+ * (concurrent streams or threads) race.
  */
 int qv_w4a16_gemm_noalloc(const void* x, const void* qweight, const void* scales,
                           const void* scaled_zeros, const void* bias, void* out,
@@ -161,6 +165,18 @@ int qv_w4a16_pack(const void* weight, const void* scales, const void* zeros,
  */
 int qv_w8a8_gemm(const int8_t* a, const int8_t* b, const void* wscales, const void* ascales,
                  const void* bias, void* out, int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * W8A8 GEMM + bias fused with a LayerScale residual update, in place:
+ * residual[M,N] = fp16(residual + gamma[n] * o), o = the fp16 output of
+ * qv_w8a8_gemm with the bias.  No reference op: a VGGT block's W8A8 proj /
+ * fc2 (w8a8_gemm_fuse_bias_forward_cuda, w8a8_gemm_cuda.cu:564-607) followed
+ * by vggt-hf's LayerScale residual add (x.addcmul_(o, gamma)), fused into the
+ * GEMM's store loop.  gamma fp16 (N), 16-byte aligned; bias required.
+ */
+int qv_w8a8_gemm_residual(const int8_t* a, const int8_t* b, const void* wscales, const void* ascales,
+                          const void* bias, const void* gamma, void* residual, int64_t M, int64_t N,
+                          int64_t K, void* stream);
 
 /*
  * The raw int32 accumulators of qv_w8a8_gemm (same kernel, no epilogue):

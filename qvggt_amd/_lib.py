@@ -38,6 +38,7 @@ SIGNATURES: dict[str, list] = {
     "qv_w4a16_gemm_qkrope": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64,
                              _vp, _vp, _vp, _vp, _f32, _i64, _vp],
     "qv_w8a8_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "qv_w8a8_gemm_residual": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "qv_w8a8_gemm_i32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "qv_quant_per_token": [_vp, _i32, _vp, _vp, _i64, _i64, _vp],
     "qv_layernorm_quant": [_vp, _i32, _vp, _vp, _vp, _vp, _f32, _i32, _i64, _i64, _vp],

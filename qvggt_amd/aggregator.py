@@ -24,9 +24,10 @@ reference's tanh gelu_and_quant).  LayerNorm eps, depth and the RoPE base
 come from ``AggregatorConfig`` (a checkpoint's config.json); its defaults are
 the benchmark configuration's LayerNorm(1024, eps 1e-6) and 24 + 24 blocks.
 
-Every hot op runs on libqvggt_hip.so; only the DINOv2 fp16 linears and the
-patch projection (plain GEMMs: hipBLASLt through torch), its GELU and the
-LayerScale residual updates use torch.
+Every hot op runs on libqvggt_hip.so, the AA blocks' LayerScale residual
+updates included (fused into the proj / fc2 GEMMs); only the DINOv2 fp16
+linears and the patch projection (plain GEMMs: hipBLASLt through torch), its
+GELU and its LayerScale residual updates use torch.
 """
 from __future__ import annotations
 
@@ -110,11 +111,15 @@ class AggregatorConfig:
 
     @classmethod
     def from_dict(cls, d: dict) -> "AggregatorConfig":
-        """Fields from a model-config dict (nested ``aggregator`` /
-        ``patch_embed`` sections are searched too); missing keys keep their
-        defaults, and ``mlp_ratio`` gives ``mlp_dim``."""
+        """Fields from a model-config dict; missing keys keep their defaults,
+        and ``mlp_ratio`` gives ``mlp_dim``.  Top-level keys and those of a
+        nested ``aggregator_config`` / ``aggregator`` section (which win) set
+        any field.  A nested ``patch_embed_config`` section describes the
+        DINOv2 patch embed only: its keys set ``dino_depth`` and
+        ``dino_ln_eps`` (its plain ``depth`` / ``layer_norm_eps`` included) and
+        never the aggregator's own blocks."""
         flat = dict(d)
-        for sec in ("aggregator_config", "aggregator", "patch_embed_config"):
+        for sec in ("aggregator_config", "aggregator"):
             if isinstance(d.get(sec), dict):
                 flat.update(d[sec])
         kw = {}
@@ -123,6 +128,14 @@ class AggregatorConfig:
                 if k in flat and flat[k] is not None:
                     kw[field] = type(getattr(cls(), field))(flat[k])
                     break
+        pe = d.get("patch_embed_config")
+        if isinstance(pe, dict):
+            for field, keys in (("dino_depth", cls._ALIASES["dino_depth"] + cls._ALIASES["depth"]),
+                                ("dino_ln_eps", cls._ALIASES["dino_ln_eps"] + cls._ALIASES["block_ln_eps"])):
+                for k in keys:
+                    if pe.get(k) is not None:
+                        kw[field] = type(getattr(cls(), field))(pe[k])
+                        break
         if "mlp_dim" not in kw and flat.get("mlp_ratio") is not None:
             kw["mlp_dim"] = int(round(float(flat["mlp_ratio"]) * kw.get("embed_dim", DIM)))
         return cls(**kw)
@@ -186,6 +199,15 @@ class W8A8Linear(nn.Module):
         else:
             E.w8a8_gemm_forward_cuda(q, self.weight, self.wscales, s, out)
         return out
+
+    def forward_residual(self, q: torch.Tensor, s: torch.Tensor, gamma: torch.Tensor,
+                         resid: torch.Tensor) -> torch.Tensor:
+        """resid += gamma * forward(q, s), in place: fused into the GEMM's
+        store loop when the layer has a bias, else the GEMM then torch's
+        addcmul (the same single rounding of resid + gamma * o)."""
+        if self.bias is not None:
+            return E.w8a8_linear_residual(q, self.weight, self.wscales, s, self.bias, gamma, resid)
+        return resid.addcmul_(self.forward(q, s), gamma)
 
 
 def quantize_w4(linear: nn.Linear, group: int = 128) -> WQLinear:
@@ -297,8 +319,7 @@ class AABlock(nn.Module):
             _linear_residual(a.proj, att, self.ls1.gamma, x, ws["o"])
         else:
             E.invoke_quant(ws["q8"], att, ws["s8"])
-            o = a.proj(ws["q8"], ws["s8"], out=ws["o"])
-            x.addcmul_(o, self.ls1.gamma)
+            a.proj.forward_residual(ws["q8"], ws["s8"], self.ls1.gamma, x)
         m = self.mlp
         if not self.w8a8:
             h = E.layer_norm(x, self.norm2.weight, self.norm2.bias, eps, out=ws["h"])
@@ -308,8 +329,7 @@ class AABlock(nn.Module):
             E.rms_norm_general(ws["q8"], x, self.norm2.weight, self.norm2.bias, ws["s8"], eps, True)
             f = m.fc1(ws["q8"], ws["s8"], out=ws["f"])
             E.gelu_and_quant(ws["q8f"], f, ws["s8"], ws["ftmp"])
-            o = m.fc2(ws["q8f"], ws["s8"], out=ws["o"])
-            x.addcmul_(o, self.ls2.gamma)
+            m.fc2.forward_residual(ws["q8f"], ws["s8"], self.ls2.gamma, x)
         return x
 
 

@@ -394,7 +394,7 @@ def _need(t: torch.Tensor, dtype, what: str, name: str):
         _fail(f"{what}: {name} must be contiguous (it is written in place)")
 
 
-def _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, what):
+def _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, what, gamma=None):
     for name, t, dt in (("in_feats", in_feats, torch.int8), ("kernel", kernel, torch.int8),
                         ("wscales", wscales, torch.float16), ("ascales", ascales, torch.float16),
                         ("out_feats", out_feats, torch.float16)):
@@ -413,10 +413,20 @@ def _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, what):
         _need(bias, torch.float16, what, "bias")
         if bias.numel() != N:
             _fail(f"{what}: bias must have N={N} elements")
-    dev = _on_gpu(in_feats, kernel, wscales, ascales, out_feats, bias, what=what)
+    if gamma is not None:
+        _need(gamma, torch.float16, what, "gamma")
+        if gamma.numel() != N:
+            _fail(f"{what}: gamma must have N={N} elements")
+        if bias is None:
+            _fail(f"{what}: the residual form needs the bias")
+    dev = _on_gpu(in_feats, kernel, wscales, ascales, out_feats, bias, gamma, what=what)
     with _device(dev):
-        _lib.call("qv_w8a8_gemm", _ptr(in_feats), _ptr(kernel), _ptr(wscales), _ptr(ascales), _ptr(bias),
-                  _ptr(out_feats), M, N, K, _stream(dev))
+        if gamma is None:
+            _lib.call("qv_w8a8_gemm", _ptr(in_feats), _ptr(kernel), _ptr(wscales), _ptr(ascales), _ptr(bias),
+                      _ptr(out_feats), M, N, K, _stream(dev))
+        else:
+            _lib.call("qv_w8a8_gemm_residual", _ptr(in_feats), _ptr(kernel), _ptr(wscales), _ptr(ascales),
+                      _ptr(bias), _ptr(gamma), _ptr(out_feats), M, N, K, _stream(dev))
 
 
 def w8a8_gemm_forward_cuda(in_feats, kernel, wscales, ascales, out_feats) -> None:
@@ -428,6 +438,17 @@ def w8a8_gemm_forward_cuda(in_feats, kernel, wscales, ascales, out_feats) -> Non
 def w8a8_gemm_fuse_bias_forward_cuda(in_feats, kernel, wscales, ascales, out_feats, bias) -> None:
     """As ``w8a8_gemm_forward_cuda`` plus bias[n] (w8a8/w8a8_gemm_cuda.cu:564-607)."""
     _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, "w8a8_gemm_fuse_bias_forward_cuda")
+
+
+def w8a8_linear_residual(in_feats, kernel, wscales, ascales, bias, gamma, residual) -> torch.Tensor:
+    """residual += gamma * fp16(W8A8 GEMM + bias), in place (one rounding of
+    residual + gamma * o in fp32): a VGGT block's W8A8 proj / fc2 fused with its
+    LayerScale residual update (``x.addcmul_(o, gamma)``).  Returns ``residual``."""
+    what = "w8a8_linear_residual"
+    if not residual.is_contiguous():
+        _fail(f"{what}: residual must be contiguous")
+    _w8a8(in_feats, kernel, wscales, ascales, residual, bias, what, gamma=gamma)
+    return residual
 
 
 def w8a8_gemm_int32(in_feats: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:

@@ -188,8 +188,10 @@ class GraphedCameraHead:
                 head(self.tokens, num_iterations)
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        # captured on the warmed-up stream: the W4 ops' per-stream split-K
-        # workspaces exist by now (none may be allocated during capture)
+        # The eager calls above made every shape's tile plan; the W4 ops'
+        # split-K launches in the graph use the device's scratch array (never
+        # an eager stream's workspace), so replays may run on any stream, but
+        # two graphs with split launches must not replay concurrently.
         with torch.cuda.graph(self.graph, stream=side):
             self.outs = head(self.tokens, num_iterations)
 

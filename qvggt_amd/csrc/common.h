@@ -141,6 +141,26 @@ __device__ __forceinline__ void pair32(float v, float& a, float& b) {
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
 }
 
+// LayerScale residual update of 8 consecutive channels (the W4A16 and W8A8
+// GEMMs' residual epilogues): r + o * g per element in fp32, o the already
+// rounded 16-bit linear output, one rounding of the result (the order of
+// torch's x.addcmul_(o, gamma) on 16-bit tensors; o * g is exact in fp32 for
+// 16-bit o and g, so a fused multiply-add gives the same value).
+template <bool BF16>
+__device__ __forceinline__ uint4 resid_update8(const uint4& r, const uint4& o, const uint4& g) {
+  const uint32_t rw[4] = {r.x, r.y, r.z, r.w}, ow[4] = {o.x, o.y, o.z, o.w}, gw[4] = {g.x, g.y, g.z, g.w};
+  uint32_t res[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = to_f32((uint16_t)(rw[i] & 0xFFFF), BF16) +
+                     to_f32((uint16_t)(ow[i] & 0xFFFF), BF16) * to_f32((uint16_t)(gw[i] & 0xFFFF), BF16);
+    const float hi = to_f32((uint16_t)(rw[i] >> 16), BF16) +
+                     to_f32((uint16_t)(ow[i] >> 16), BF16) * to_f32((uint16_t)(gw[i] >> 16), BF16);
+    res[i] = pack2<BF16>(lo, hi);
+  }
+  return make_uint4(res[0], res[1], res[2], res[3]);
+}
+
 // Byte offset of (row, byte) in a GEMM epilogue staging area of 128-byte rows
 // (a wave's 64-channel fp16 output tile): 16-byte chunk c of row r sits at
 // c ^ ((r >> 1) & 7).  The staging writes (8 bytes, one row per lane, the same

@@ -4,7 +4,8 @@
 // (rope_new/fused_rope_with_pos.cu:19-164): rotate-half RoPE on the first d2
 // dims of x[s][b][h][:] (arbitrary element strides) with fp32 angles
 // freqs[b][s][0:d2]; dims >= d2 are copied.  cos/sin are evaluated in fp64 and
-// rounded to fp32 (the reference used the fast-math sincosf).
+// rounded to fp32 (the reference used the fast-math sincosf), once per
+// (s, b, d) and shared by the heads.
 //
 // qv_rope2d: the VGGT 2-D RoPE on the q and k parts of a fused qkv buffer
 // (tokens, 3, H, 64).  Head dims [0,32) rotate with the token's y position,
@@ -30,37 +31,121 @@ __device__ __forceinline__ void st1(void* p, size_t i, float v) {
   else reinterpret_cast<uint16_t*>(p)[i] = from_f32<DT == QV_BF16>(v);
 }
 
-// One thread per (s, b, h, j): j < d2/2 rotates the pair (j, j + d2/2); the
-// threads with j >= d2/2 copy the pass-through dims.
+// Eight elements at e of a 16- or 32-bit row, as fp32 (16-byte aligned).
 template <int DT>
-__global__ __launch_bounds__(256) void rope_with_pos_kernel(
-    const void* __restrict__ x, const float* __restrict__ freqs, void* __restrict__ out, int S, int B, int H,
-    int D, int D2, long sx_s, long sx_b, long sx_h, long sx_d, long so_s, long so_b, long so_h, long so_d,
-    int per_head) {
-  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
-  const long total = (long)S * B * H * per_head;
-  if (gid >= total) return;
-  const int j = (int)(gid % per_head);
-  long r = gid / per_head;
-  const int hh = (int)(r % H);
-  r /= H;
-  const int bb = (int)(r % B);
-  const int ss = (int)(r / B);
-  const long xi = ss * sx_s + bb * sx_b + hh * sx_h;
-  const long oi = ss * so_s + bb * so_b + hh * so_h;
-  const int half = D2 / 2;
-  if (j < half) {
-    const float* f = freqs + ((long)bb * S + ss) * D2;
-    const float a = ld1<DT>(x, xi + j * sx_d);
-    const float p = ld1<DT>(x, xi + (j + half) * sx_d);
-    const double th0 = (double)f[j], th1 = (double)f[j + half];
-    const float c0 = (float)cos(th0), s0 = (float)sin(th0);
-    const float c1 = (float)cos(th1), s1 = (float)sin(th1);
-    st1<DT>(out, oi + j * so_d, a * c0 + (-p) * s0);
-    st1<DT>(out, oi + (j + half) * so_d, p * c1 + a * s1);
+__device__ __forceinline__ void ld8(const void* p, long e, float (&v)[8]) {
+  if constexpr (DT == QV_F32) {
+    const uint4 a = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p) + e);
+    const uint4 b = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p) + e + 4);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_bit_cast(float, w[i]);
   } else {
-    for (int d = D2 + (j - half); d < D; d += per_head - half)
-      st1<DT>(out, oi + d * so_d, ld1<DT>(x, xi + d * sx_d));
+    const uint4 u = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + e);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = to_f32((uint16_t)(w[i] & 0xFFFF), DT == QV_BF16);
+      v[2 * i + 1] = to_f32((uint16_t)(w[i] >> 16), DT == QV_BF16);
+    }
+  }
+}
+template <int DT>
+__device__ __forceinline__ void st8(void* p, long e, const float (&v)[8]) {
+  if constexpr (DT == QV_F32) {
+    float* q = reinterpret_cast<float*>(p) + e;
+    *reinterpret_cast<uint4*>(q) = make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                                              __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+    *reinterpret_cast<uint4*>(q + 4) = make_uint4(__builtin_bit_cast(uint32_t, v[4]), __builtin_bit_cast(uint32_t, v[5]),
+                                                  __builtin_bit_cast(uint32_t, v[6]), __builtin_bit_cast(uint32_t, v[7]));
+  } else {
+    constexpr bool BF = DT == QV_BF16;
+    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p) + e) =
+        make_uint4(pack2<BF>(v[0], v[1]), pack2<BF>(v[2], v[3]), pack2<BF>(v[4], v[5]), pack2<BF>(v[6], v[7]));
+  }
+}
+
+// qv_rope_with_pos.  One wave per (s, b) position at a time (grid-stride).
+// The rotation angles freqs[b][s][0, d2) are the same for all H heads of a
+// position, so the wave first evaluates their cos / sin once (fp64, rounded
+// to fp32) into a wave-private LDS row, then rotates the heads from it.
+// VEC (unit element stride of the head dims in x and out, 16-byte aligned
+// rows, d2/2 and d - d2 multiples of 8): a lane moves 8 dims of the first
+// half and their 8 partners of the second half with 16-byte accesses, then
+// the pass-through dims in 8-element chunks; otherwise a lane takes one
+// (head, pair) at a time with element accesses.  d2 above RWP_MAX_D2 skips
+// the table and evaluates cos / sin per element.
+constexpr int RWP_WAVES = 4;
+constexpr int RWP_MAX_D2 = 512;
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(64 * RWP_WAVES) void rope_with_pos_kernel(
+    const void* __restrict__ x, const float* __restrict__ freqs, void* __restrict__ out, int S, int B, int H,
+    int D, int D2, long sx_s, long sx_b, long sx_h, long sx_d, long so_s, long so_b, long so_h, long so_d) {
+  __shared__ float cs_l[RWP_WAVES][RWP_MAX_D2], sn_l[RWP_WAVES][RWP_MAX_D2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = D2 / 2;
+  const bool tab = D2 <= RWP_MAX_D2;
+  float* cs = cs_l[wave];
+  float* sn = sn_l[wave];
+  const long npos = (long)S * B;
+  for (long pidx = (long)blockIdx.x * RWP_WAVES + wave; pidx < npos; pidx += (long)gridDim.x * RWP_WAVES) {
+    const int ss = (int)(pidx / B), bb = (int)(pidx % B);
+    const float* f = freqs + ((long)bb * S + ss) * D2;
+    auto cosv = [&](int d) { return tab ? cs[d] : (float)cos((double)f[d]); };
+    auto sinv = [&](int d) { return tab ? sn[d] : (float)sin((double)f[d]); };
+    if (tab) {
+      for (int d = lane; d < D2; d += 64) {
+        const double th = (double)f[d];
+        cs[d] = (float)cos(th);
+        sn[d] = (float)sin(th);
+      }
+      // the wave's LDS accesses run in order: make the compiler keep them so
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+    const long xb = ss * sx_s + bb * sx_b, ob = ss * so_s + bb * so_b;
+    if constexpr (VEC) {
+      const int nch = half >> 3;
+      for (int t = lane; t < H * nch; t += 64) {
+        const int hh = t / nch, c = 8 * (t - hh * nch);
+        float a[8], pp[8], o1[8], o2[8];
+        ld8<DT>(x, xb + hh * sx_h + c, a);
+        ld8<DT>(x, xb + hh * sx_h + half + c, pp);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          o1[e] = a[e] * cosv(c + e) + (-pp[e]) * sinv(c + e);
+          o2[e] = pp[e] * cosv(half + c + e) + a[e] * sinv(half + c + e);
+        }
+        st8<DT>(out, ob + hh * so_h + c, o1);
+        st8<DT>(out, ob + hh * so_h + half + c, o2);
+      }
+      const int npass = (D - D2) >> 3;
+      for (int t = lane; t < H * npass; t += 64) {
+        const int hh = t / npass, c = D2 + 8 * (t - hh * npass);
+        float v[8];
+        ld8<DT>(x, xb + hh * sx_h + c, v);
+        st8<DT>(out, ob + hh * so_h + c, v);
+      }
+    } else {
+      for (int t = lane; t < H * half; t += 64) {
+        const int hh = t / half, j = t - hh * half;
+        const long xi = xb + hh * sx_h, oi = ob + hh * so_h;
+        const float a = ld1<DT>(x, xi + j * sx_d);
+        const float pp = ld1<DT>(x, xi + (j + half) * sx_d);
+        st1<DT>(out, oi + j * so_d, a * cosv(j) + (-pp) * sinv(j));
+        st1<DT>(out, oi + (j + half) * so_d, pp * cosv(j + half) + a * sinv(j + half));
+      }
+      const int npass = D - D2;
+      for (int t = lane; t < H * npass; t += 64) {
+        const int hh = t / npass, d = D2 + (t - hh * npass);
+        st1<DT>(out, ob + hh * so_h + d * so_d, ld1<DT>(x, xb + hh * sx_h + d * sx_d));
+      }
+    }
+    if (tab) {
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // reads done before the next position's writes
+      __builtin_amdgcn_wave_barrier();
+    }
   }
 }
 
@@ -282,24 +367,30 @@ extern "C" int qv_rope_with_pos(const void* x, const float* freqs, void* out, in
   QV_CHECK_ARG(x_strides && out_strides, "null stride array");
   if (S * B * H == 0) return QV_OK;
   QV_CHECK_ARG(x && freqs && out, "null pointer argument");
-  const int half = (int)(D2 / 2);
-  // rotating threads (one per pair) + up to 64 copy threads for dims >= d2
-  const int extra = D > D2 ? (int)(D - D2 < 64 ? D - D2 : 64) : 0;
-  const int per_head = half + extra;
-  const long total = (long)S * B * H * per_head;
-  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
-  hipStream_t st = (hipStream_t)stream;
+  QV_CHECK_ARG(S <= INT32_MAX && B <= INT32_MAX && H * D <= INT32_MAX, "shape too large");
+  QV_CHECK_ARG(dtype == QV_F16 || dtype == QV_BF16 || dtype == QV_F32, "unsupported dtype %d", dtype);
   const long* xs = (const long*)x_strides;
   const long* os = (const long*)out_strides;
-#define QV_ROPE(DTV)                                                                                        \
-  hipLaunchKernelGGL((rope_with_pos_kernel<DTV>), grid, block, 0, st, x, freqs, out, (int)S, (int)B, (int)H, \
-                     (int)D, (int)D2, xs[0], xs[1], xs[2], xs[3], os[0], os[1], os[2], os[3], per_head)
+  // 16-byte vector accesses: unit dim strides, aligned rows, whole 8-element chunks
+  const long align = dtype == QV_F32 ? 4 : 8;
+  const bool vec = xs[3] == 1 && os[3] == 1 && (D2 / 2) % 8 == 0 && (D - D2) % 8 == 0 &&
+                   xs[0] % align == 0 && xs[1] % align == 0 && xs[2] % align == 0 && os[0] % align == 0 &&
+                   os[1] % align == 0 && os[2] % align == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)out % 16) == 0;
+  const long npos = S * B;
+  const long blocks = (npos + RWP_WAVES - 1) / RWP_WAVES;
+  const dim3 grid((unsigned)(blocks < 16384 ? blocks : 16384)), block(64 * RWP_WAVES);
+  hipStream_t st = (hipStream_t)stream;
+#define QV_ROPE(DTV, V)                                                                                        \
+  hipLaunchKernelGGL((rope_with_pos_kernel<DTV, V>), grid, block, 0, st, x, freqs, out, (int)S, (int)B, (int)H, \
+                     (int)D, (int)D2, xs[0], xs[1], xs[2], xs[3], os[0], os[1], os[2], os[3])
+#define QV_ROPE_DT(DTV) \
+  if (vec) QV_ROPE(DTV, true); else QV_ROPE(DTV, false);
   switch (dtype) {
-    case QV_F16: QV_ROPE(QV_F16); break;
-    case QV_BF16: QV_ROPE(QV_BF16); break;
-    case QV_F32: QV_ROPE(QV_F32); break;
-    default: set_error("unsupported dtype %d", dtype); return QV_EINVAL;
+    case QV_F16: QV_ROPE_DT(QV_F16) break;
+    case QV_BF16: QV_ROPE_DT(QV_BF16) break;
+    default: QV_ROPE_DT(QV_F32) break;
   }
+#undef QV_ROPE_DT
 #undef QV_ROPE
   return check_launch("rope_with_pos");
 }

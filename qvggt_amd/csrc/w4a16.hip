@@ -35,10 +35,15 @@ namespace qv {
 // blocks (e.g. 8192 -> 2048: 128 blocks) still fills the CUs.  Each split
 // writes its fp32 partial (M x 16 NB) to workspace slot (b, ks) with
 // agent-coherent (sc1) stores, waits for them (vmcnt 0) and bumps block b's
-// arrival counter; the split that arrives last reads the SK partials back in
-// ks order -- the sum order never depends on arrival order -- runs the
-// epilogue and resets the counter to zero for the next launch.  No workgroup
-// waits on another.
+// arrival counter with a wrapping increment (global_atomic_inc with limit
+// SK - 1: SK - 1 -> 0), so the split that sees SK - 1 arrives last and the
+// same atomic has already returned the counter to zero for the next launch.
+// The counters of one SK serve only launches with that SK (cnt points at
+// that range), so every launch adds exactly SK increments to each counter it
+// touches and leaves it as it found it, even if launches that wrongly share
+// a workspace overlap.  The last split reads the SK partials back in ks
+// order -- the sum order never depends on arrival order -- and runs the
+// epilogue.  No workgroup waits on another.
 template <bool BF16, int MB, int NB>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB == 1 ? 8 : 1))) void w4a16_skinny_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
@@ -189,10 +194,11 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
   if (SK == 1) return;
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial values are stored
   __syncthreads();
-  if (tid == 0) s_arrived = __hip_atomic_fetch_add(cnt + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0)
+    s_arrived = (int)__builtin_amdgcn_atomic_inc32(reinterpret_cast<unsigned*>(cnt) + blockIdx.x, (unsigned)(SK - 1),
+                                                   __ATOMIC_RELAXED, "agent");
   __syncthreads();
   if (s_arrived != SK - 1) return;   // another split finishes the block
-  if (tid == 0) __hip_atomic_exchange(cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (int e = tid; e < M * 16 * NB; e += blockDim.x) {
     const int m = e / (16 * NB), cn = e % (16 * NB), j = cn >> 4, c = cn & 15;
     // the partials of up to four splits are loaded together (one L2 round
@@ -524,9 +530,12 @@ StreamPlan w4_plan_for(int tile, int M, int N, int K, int epi) {
 }
 }  // namespace
 
-// Split-K workspace of the skinny kernel: fp32 partials and one arrival
-// counter per channel block (zero between launches: the finishing split
-// resets it).
+// Split-K workspace of the skinny kernel: fp32 partials and the arrival
+// counters, SPLIT_MAX_BLOCKS per split factor (2 and 4: counters
+// [0, 256) serve two-way launches, [256, 512) four-way ones).  The counters
+// start at zero (cleared when the workspace is made) and every complete
+// launch returns each counter it uses to zero with its last wrapping
+// increment (see w4a16_skinny_kernel), so no launch clears them.
 struct SplitWorkspace {
   float* part = nullptr;
   int* cnt = nullptr;
@@ -534,15 +543,16 @@ struct SplitWorkspace {
   int cnt_n = 0;
 };
 constexpr size_t SPLIT_PART_FLOATS = (size_t)2 << 20;   // 8 MiB of partials
-constexpr int SPLIT_COUNTERS = 4096;                     // channel blocks (N <= 65536)
+constexpr int SPLIT_MAX_BLOCKS = 256;                    // a split launch has < 256 channel blocks
+constexpr int SPLIT_COUNTERS = 4096;                     // >= 2 x SPLIT_MAX_BLOCKS
+static_assert(SPLIT_COUNTERS >= 2 * SPLIT_MAX_BLOCKS, "one counter range per split factor");
 
 static int split_workspace(hipStream_t st, SplitWorkspace& ws);
 
 template <bool BF16>
 static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
-                         void* out, int M, int N, int K, int epi, hipStream_t st,
-                         const void* gamma = nullptr, const SplitWorkspace* ws = nullptr, int nb_force = 0,
-                         int sk_force = 0);
+                         void* out, int M, int N, int K, int epi, hipStream_t st, const void* gamma,
+                         const SplitWorkspace& ws);
 
 template <bool BF16>
 static int launch_gemm(const void* x, const void* qw, const void* s, const void* z, const void* bias,
@@ -552,7 +562,7 @@ static int launch_gemm(const void* x, const void* qw, const void* s, const void*
     SplitWorkspace ws;
     const int rc = split_workspace(st, ws);
     if (rc) return rc;
-    return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st, gamma, ws.part ? &ws : nullptr);
+    return launch_skinny<BF16>(x, qw, s, z, bias, out, M, N, K, epi, st, gamma, ws);
   }
   return launch_w4a16_stream<BF16>(x, qw, s, z, bias, gamma, out, M, N, K, epi, w4_plan_for(tile, M, N, K, epi), st);
 }
@@ -571,36 +581,44 @@ static int w4_skinny_nb(int M, int N) {
 // 32-channel blocks, which halves the activation re-reads.  Measured from
 // graph replays over > 1 GB of rotating weights (8192 -> 2048: M = 32
 // 19.9 -> 10.5 us, M = 8 8.1 -> 7.2 us, M = 1 6.4 -> 6.2 us); splitting K <= 2048
-// or shapes that already give >= 256 blocks measured equal or slower.
-static void w4_skinny_plan(int M, int N, int K, const SplitWorkspace* ws, int& nb, int& sk) {
+// or shapes that already give >= 256 blocks measured equal or slower.  A
+// split that the workspace cannot hold (partials or counters) runs unsplit.
+static void w4_skinny_plan(int M, int N, int K, const SplitWorkspace& ws, int& nb, int& sk) {
   nb = w4_skinny_nb(M, N);
   sk = 1;
-  if (!ws || K / 128 < 64 || N / (16 * nb) >= 256) return;
+  if (K / 128 < 64 || N / (16 * nb) >= SPLIT_MAX_BLOCKS) return;
   if (M > 8 && N % 32 == 0) {
     nb = 2;
     sk = 4;
   } else {
     sk = 2;
   }
-  if ((size_t)N * M * sk > ws->part_floats || N / (16 * nb) > ws->cnt_n) {
+  if ((size_t)N * M * sk > ws.part_floats || N / (16 * nb) >= SPLIT_MAX_BLOCKS) {
     nb = w4_skinny_nb(M, N);
     sk = 1;
   }
 }
 
+// zero n counters of a new workspace (a kernel on the stream that will use
+// it, not a synchronous memset on the null stream)
+__global__ __launch_bounds__(256) void zero_counters_kernel(int* __restrict__ c, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) c[i] = 0;
+}
+
 template <bool BF16>
 static int launch_skinny(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                          void* out, int M, int N, int K, int epi, hipStream_t st, const void* gamma,
-                         const SplitWorkspace* ws, int nb_force, int sk_force) {
+                         const SplitWorkspace& ws) {
   int nb, sk;
   w4_skinny_plan(M, N, K, ws, nb, sk);
-  if (nb_force > 0) nb = nb_force;
-  if (sk_force > 0 && ws) sk = sk_force;
   const int KT = K / 128 / sk;
   const int waves = KT < 16 ? KT : 16;
   const dim3 grid(N / (16 * nb), sk), block(64 * waves);
-  float* part = sk > 1 ? ws->part : nullptr;
-  int* cnt = sk > 1 ? ws->cnt : nullptr;
+  float* part = sk > 1 ? ws.part : nullptr;
+  int* cnt = sk > 1 ? ws.cnt + (sk == 2 ? 0 : SPLIT_MAX_BLOCKS) : nullptr;
+  QV_CHECK_ARG(sk == 1 || ((sk == 2 || sk == 4) && (int)grid.x < SPLIT_MAX_BLOCKS && ws.cnt_n >= 2 * SPLIT_MAX_BLOCKS),
+               "w4a16 skinny: bad split plan (%d splits over %d blocks)", sk, (int)grid.x);
 #define QV_SKINNY(MB, NB)                                                                         \
   hipLaunchKernelGGL((w4a16_skinny_kernel<BF16, MB, NB>), grid, block, 0, st, (const uint16_t*)x, \
                      (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,                 \
@@ -610,64 +628,28 @@ static int launch_skinny(const void* x, const void* qw, const void* s, const voi
   else if (M <= 32) QV_SKINNY(2, NB); \
   else if (M <= 48) QV_SKINNY(3, NB); \
   else QV_SKINNY(4, NB);
-  if (nb == 4) { QV_SKINNY_M(4) }
-  else if (nb == 2) { QV_SKINNY_M(2) }
+  if (nb == 2) { QV_SKINNY_M(2) }
   else { QV_SKINNY_M(1) }
 #undef QV_SKINNY_M
 #undef QV_SKINNY
   return check_launch("w4a16_skinny");
 }
 
-// One split workspace per (device, stream), allocated on first use and
-// zeroed then: launches on one stream run in order and share it; another
-// stream gets its own.  A stream that is being captured into a graph and has
-// none yet gets none (the launch runs unsplit), since allocation is not
-// allowed during capture; the no-allocation entry point covers that case.
-static int split_workspace(hipStream_t st, SplitWorkspace& ws) {
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, SplitWorkspace> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    set_error("w4a16 skinny: hipGetDevice failed");
-    return QV_EHIP;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair(dev, st);
-  const auto it = cache.find(key);
-  if (it != cache.end()) {
-    ws = it->second;
-    return QV_OK;
-  }
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    ws = SplitWorkspace();
-    return QV_OK;
-  }
-  SplitWorkspace n;
-  n.part_floats = SPLIT_PART_FLOATS;
-  n.cnt_n = SPLIT_COUNTERS;
-  if (hipMalloc(&n.part, n.part_floats * sizeof(float)) != hipSuccess ||
-      hipMalloc(&n.cnt, n.cnt_n * sizeof(int)) != hipSuccess ||
-      hipMemset(n.cnt, 0, n.cnt_n * sizeof(int)) != hipSuccess) {
-    set_error("w4a16 skinny: split workspace allocation failed (%s)", hipGetErrorString(hipGetLastError()));
-    return QV_EHIP;
-  }
-  cache[key] = n;
-  ws = n;
-  return QV_OK;
-}
-
-// ------------------------------------------------- no-allocation variant
-// File-scope device scratch for qv_w4a16_gemm_noalloc: the split partials and
-// counters of SplitWorkspace, fixed at 8 MiB + 16 KiB per GPU for the life of
-// the process.  In host code `scratch` only names the symbol; its device
-// address comes from hipGetSymbolAddress, once per device with that device
-// current (scratch_workspace), and only that address is passed to kernels.
-// Calls that overlap on one GPU share the array and so race.
+// ------------------------------------------------- device scratch
+// File-scope device scratch: the split partials and counters of a
+// SplitWorkspace, fixed at 8 MiB + 16 KiB per GPU for the life of the
+// process.  qv_w4a16_gemm_noalloc always uses it; the allocating entries use
+// it for a launch captured into a graph on a stream that has no workspace of
+// its own yet (see split_workspace).  In host code `scratch` only names the
+// symbol; its device address comes from hipGetSymbolAddress, once per device
+// with that device current (scratch_workspace), and only that address is
+// passed to kernels.  That first call also clears the counters (a kernel on
+// the caller's stream, then a wait for it), so it has to run outside stream
+// capture.  Split launches that overlap on one GPU and use the scratch share
+// it and so race.
 static __device__ __align__(256) uint8_t scratch[SPLIT_PART_FLOATS * sizeof(float) + SPLIT_COUNTERS * sizeof(int)];
 
-static int scratch_workspace(SplitWorkspace& ws) {
+static int scratch_workspace(hipStream_t st, SplitWorkspace& ws) {
   constexpr int MAX_DEV = 64;
   static std::mutex mu;
   static void* ptr[MAX_DEV] = {};
@@ -678,10 +660,27 @@ static int scratch_workspace(SplitWorkspace& ws) {
   }
   std::lock_guard<std::mutex> lock(mu);
   if (!ptr[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+      set_error("w4a16 skinny: hipStreamIsCapturing failed (%s)", hipGetErrorString(hipGetLastError()));
+      return QV_EHIP;
+    }
+    QV_CHECK_ARG(cap == hipStreamCaptureStatusNone,
+                 "w4a16 skinny: the first split-K call on a device clears the device scratch and must run "
+                 "outside stream capture (make one eager call first)");
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) {
       set_error("w4a16 no-alloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+      return QV_EHIP;
+    }
+    int* cnt = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(p) + SPLIT_PART_FLOATS * sizeof(float));
+    hipLaunchKernelGGL(zero_counters_kernel, dim3((SPLIT_COUNTERS + 255) / 256), dim3(256), 0, st, cnt,
+                       SPLIT_COUNTERS);
+    const int rc = check_launch("zero_counters");
+    if (rc) return rc;
+    if (hipStreamSynchronize(st) != hipSuccess) {
+      set_error("w4a16 skinny: clearing the device scratch failed (%s)", hipGetErrorString(hipGetLastError()));
       return QV_EHIP;
     }
     ptr[dev] = p;
@@ -693,11 +692,60 @@ static int scratch_workspace(SplitWorkspace& ws) {
   return QV_OK;
 }
 
-// zero n counters (a kernel, not hipMemsetAsync, so the call can be captured
-// into a graph)
-__global__ __launch_bounds__(256) void zero_counters_kernel(int* __restrict__ c, int n) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < n) c[i] = 0;
+// Eager launches: one split workspace per (device, stream), allocated on the
+// stream's first skinny call; launches on one stream run in order and share
+// it, another stream gets its own, so eager skinny calls on different streams
+// may overlap.  Launches captured into a graph always use the device scratch
+// instead: capture cannot allocate, the split plan (and with it every output
+// bit) is then the same as an eager call's, and a graph -- which keeps the
+// workspace it was captured with and may be replayed on any stream -- never
+// shares memory with eager calls.  Graphs with split launches that are
+// replayed concurrently with each other (or with qv_w4a16_gemm_noalloc
+// calls) on one GPU race.
+static int split_workspace(hipStream_t st, SplitWorkspace& ws) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, SplitWorkspace> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("w4a16 skinny: hipGetDevice failed");
+    return QV_EHIP;
+  }
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+    set_error("w4a16 skinny: hipStreamIsCapturing failed (%s)", hipGetErrorString(hipGetLastError()));
+    return QV_EHIP;
+  }
+  if (cap != hipStreamCaptureStatusNone) return scratch_workspace(st, ws);
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(std::make_pair(dev, st));
+    if (it != cache.end()) {
+      ws = it->second;
+      return QV_OK;
+    }
+  }
+  // set the device scratch up now, outside capture, for a later capture on a
+  // stream that has no workspace
+  SplitWorkspace sc;
+  int rc = scratch_workspace(st, sc);
+  if (rc) return rc;
+  SplitWorkspace n;
+  n.part_floats = SPLIT_PART_FLOATS;
+  n.cnt_n = SPLIT_COUNTERS;
+  if (hipMalloc(&n.part, n.part_floats * sizeof(float)) != hipSuccess ||
+      hipMalloc(&n.cnt, n.cnt_n * sizeof(int)) != hipSuccess) {
+    set_error("w4a16 skinny: split workspace allocation failed (%s)", hipGetErrorString(hipGetLastError()));
+    return QV_EHIP;
+  }
+  // the counters start at zero; only this stream (and graphs captured on it)
+  // will use them, after this kernel
+  hipLaunchKernelGGL(zero_counters_kernel, dim3((n.cnt_n + 255) / 256), dim3(256), 0, st, n.cnt, n.cnt_n);
+  rc = check_launch("zero_counters");
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(mu);
+  cache[std::make_pair(dev, st)] = n;
+  ws = n;
+  return QV_OK;
 }
 
 static int check_common(const void* x, const void* qw, const void* s, const void* z, const void* bias,
@@ -749,12 +797,11 @@ extern "C" int qv_w4a16_gemv(const void* x, const void* qweight, const void* sca
   SplitWorkspace ws;
   rc = split_workspace(st, ws);
   if (rc) return rc;
-  const SplitWorkspace* w = ws.part ? &ws : nullptr;
   if (dtype == QV_BF16)
     return launch_skinny<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st,
-                               nullptr, w);
+                               nullptr, ws);
   return launch_skinny<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st,
-                              nullptr, w);
+                              nullptr, ws);
 }
 
 extern "C" int qv_w4a16_dequant(const void* qweight, const void* scales, const void* scaled_zeros,
@@ -882,9 +929,6 @@ extern "C" int qv_w4a16_gemm_noalloc(const void* x, const void* qweight, const v
                                      int64_t N, int64_t K, int dtype, int epilogue, void* stream) {
   int rc = check_common(x, qweight, scales, scaled_zeros, bias, out, M, N, K, dtype, epilogue);
   if (rc) return rc;
-  QV_CHECK_ARG(N <= (int64_t)SPLIT_COUNTERS * 16,
-               "N=%lld exceeds the no-allocation limit %d (one counter per 16 channels in a fixed scratch)",
-               (long long)N, SPLIT_COUNTERS * 16);
   if (M == 0) return QV_OK;
   hipStream_t st = (hipStream_t)stream;
   if (w4_pick_tile((int)M, (int)N, (int)K) != 5) {   // the large-M kernels use no scratch
@@ -892,20 +936,14 @@ extern "C" int qv_w4a16_gemm_noalloc(const void* x, const void* qweight, const v
       return launch_gemm<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
     return launch_gemm<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st);
   }
+  // The skinny path splits K into the scratch when its plan fits there
+  // (w4_skinny_plan runs every other shape unsplit, as qv_w4a16_gemm does).
   SplitWorkspace ws;
-  rc = scratch_workspace(ws);
+  rc = scratch_workspace(st, ws);
   if (rc) return rc;
-  int nb, sk;
-  w4_skinny_plan((int)M, (int)N, (int)K, &ws, nb, sk);
-  if (sk > 1) {
-    const int blocks = (int)(N / (16 * nb));
-    hipLaunchKernelGGL(zero_counters_kernel, dim3((blocks + 255) / 256), dim3(256), 0, st, ws.cnt, blocks);
-    rc = check_launch("zero_counters");
-    if (rc) return rc;
-  }
   if (dtype == QV_BF16)
     return launch_skinny<true>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st,
-                               nullptr, &ws);
+                               nullptr, ws);
   return launch_skinny<false>(x, qweight, scales, scaled_zeros, bias, out, (int)M, (int)N, (int)K, epilogue, st,
-                              nullptr, &ws);
+                              nullptr, ws);
 }

@@ -140,24 +140,6 @@ __device__ __forceinline__ void epilogue_apply4(const uint16_t* __restrict__ bia
   }
 }
 
-// Residual update of 8 consecutive channels: r + o * g per element in fp32,
-// o the already rounded 16-bit linear output, one rounding of the result (the
-// order of torch's x.addcmul_(o, gamma) on 16-bit tensors).
-template <bool BF16>
-__device__ __forceinline__ uint4 resid_update8(const uint4& r, const uint4& o, const uint4& g) {
-  const uint32_t rw[4] = {r.x, r.y, r.z, r.w}, ow[4] = {o.x, o.y, o.z, o.w}, gw[4] = {g.x, g.y, g.z, g.w};
-  uint32_t res[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float lo = to_f32((uint16_t)(rw[i] & 0xFFFF), BF16) +
-                     to_f32((uint16_t)(ow[i] & 0xFFFF), BF16) * to_f32((uint16_t)(gw[i] & 0xFFFF), BF16);
-    const float hi = to_f32((uint16_t)(rw[i] >> 16), BF16) +
-                     to_f32((uint16_t)(ow[i] >> 16), BF16) * to_f32((uint16_t)(gw[i] >> 16), BF16);
-    res[i] = pack2<BF16>(lo, hi);
-  }
-  return make_uint4(res[0], res[1], res[2], res[3]);
-}
-
 // Bias / GELU epilogue on four consecutive channels n..n+3 of token m, one
 // rounding to the 16-bit output type, one 8-byte store.
 template <bool BF16, int EPI>

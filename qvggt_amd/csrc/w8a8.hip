@@ -16,7 +16,10 @@
 // (16 contiguous bytes = chunk 2s + h) on both operands.  Output: lane (h, l),
 // register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the wave's tile.
 // Outputs are written with non-temporal stores so that they do not evict the
-// operand rows the XCD's other tiles still read from L2.
+// operand rows the XCD's other tiles still read from L2.  The residual form
+// (OUT 3, qv_w8a8_gemm_residual) reads the residual row chunk and LayerScale
+// gamma in the store loop and writes residual + gamma * fp16(epilogue) in
+// place, which replaces torch's x.addcmul_(o, gamma) pass of a VGGT block.
 #include "common.h"
 
 #pragma clang fp contract(off)
@@ -25,12 +28,15 @@ namespace qv {
 
 __device__ __forceinline__ int f8(int r) { return (r + (r >> 2)) & 3; }
 
-template <int MT, int OUT>  // OUT: 0 = fp16 (scaled), 1 = fp16 (scaled + bias), 2 = raw int32
+// OUT: 0 = fp16 (scaled), 1 = fp16 (scaled + bias), 2 = raw int32,
+// 3 = fp16 (scaled + bias) LayerScale-added to `out` in place
+template <int MT, int OUT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b,
                       const uint16_t* __restrict__ ws, const uint16_t* __restrict__ as,
-                      const uint16_t* __restrict__ bias, void* __restrict__ out, int M, int N, int K,
-                      int tiles_n, int gn) {
+                      const uint16_t* __restrict__ bias, const uint16_t* __restrict__ gamma,
+                      void* __restrict__ out, int M, int N, int K, int tiles_n, int gn) {
+  constexpr bool BIAS = OUT == 1 || OUT == 3;
   constexpr int BM = 32 * MT, BN = 256, NT = 2;
   constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64;
   constexpr int STAGE = A_BYTES + B_BYTES;
@@ -75,7 +81,7 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
       for (int qd = 0; qd < 4; ++qd) {
         const int n = min(n0 + 64 * wave + 32 * j + 8 * qd + 4 * h, N - 4);
         wsv[j][qd] = *reinterpret_cast<const uint2*>(ws + n);
-        if constexpr (OUT == 1) bsv[j][qd] = *reinterpret_cast<const uint2*>(bias + n);
+        if constexpr (BIAS) bsv[j][qd] = *reinterpret_cast<const uint2*>(bias + n);
       }
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -206,7 +212,7 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
         wsn[1] = to_f32((uint16_t)(wv.x >> 16), false);
         wsn[2] = to_f32((uint16_t)(wv.y & 0xFFFF), false);
         wsn[3] = to_f32((uint16_t)(wv.y >> 16), false);
-        if constexpr (OUT == 1) {
+        if constexpr (BIAS) {
           uint2 bv;
           if constexpr (PREF) bv = bsv[j][qd];
           else bv = *reinterpret_cast<const uint2*>(bias + n);
@@ -222,7 +228,7 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
           for (int e = 0; e < 4; ++e) {
             float t = (float)acc[j][i][4 * qd + e] * wsn[e];
             t = t * am[i];
-            if constexpr (OUT == 1) t = t + bn[e];
+            if constexpr (BIAS) t = t + bn[e];
             // keep the fp32 rounding of t: without this the backend fuses the last
             // multiply and the fp16 conversion into one v_fma_mixlo_f16 (one rounding)
             asm volatile("" : "+v"(t));
@@ -243,8 +249,13 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
       const int idx = it * 64 + lane;
       const int row = idx >> 3, c = idx & 7;
       const int m = m0 + row, n = n0 + 64 * wave + 8 * c;
-      if (m < M && n < N)
-        st_stream16(o16 + (size_t)m * N + n, *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16)));
+      if (m < M && n < N) {
+        uint4 v = *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16));
+        if constexpr (OUT == 3)
+          v = resid_update8<false>(*reinterpret_cast<const uint4*>(o16 + (size_t)m * N + n), v,
+                                   *reinterpret_cast<const uint4*>(gamma + n));
+        st_stream16(o16 + (size_t)m * N + n, v);
+      }
     }
   }
 }
@@ -275,36 +286,42 @@ static int w8a8_col_group(long tiles_m, int tiles_n, long M, long K) {
 }
 
 template <int MT, int OUT>
-static void launch(const void* a, const void* b, const void* ws, const void* as, const void* bias, void* out,
-                   int M, int N, int K, hipStream_t st) {
+static void launch(const void* a, const void* b, const void* ws, const void* as, const void* bias,
+                   const void* gamma, void* out, int M, int N, int K, hipStream_t st) {
   const int tiles_m = (M + 32 * MT - 1) / (32 * MT), tiles_n = (N + 255) / 256;
   const int gn = w8a8_col_group(tiles_m, tiles_n, M, K);
   hipLaunchKernelGGL((w8a8_gemm_kernel<MT, OUT>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
                      (const int8_t*)a, (const int8_t*)b, (const uint16_t*)ws, (const uint16_t*)as,
-                     (const uint16_t*)bias, out, M, N, K, tiles_n, gn);
+                     (const uint16_t*)bias, (const uint16_t*)gamma, out, M, N, K, tiles_n, gn);
 }
 
-static int w8a8_run(const void* a, const void* b, const void* ws, const void* as, const void* bias, void* out,
-                    int64_t M, int64_t N, int64_t K, int mode, void* stream) {
+// mode: 0 = fp16 out, 1 = fp16 out + bias, 2 = int32 accumulators,
+// 3 = bias + LayerScale residual into `out` (the residual stream)
+static int w8a8_run(const void* a, const void* b, const void* ws, const void* as, const void* bias,
+                    const void* gamma, void* out, int64_t M, int64_t N, int64_t K, int mode, void* stream) {
   QV_CHECK_ARG(M >= 0 && N > 0 && K > 0, "bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   QV_CHECK_ARG(K % 64 == 0, "K=%lld must be a multiple of 64", (long long)K);
   QV_CHECK_ARG(N % 16 == 0, "N=%lld must be a multiple of 16", (long long)N);
   QV_CHECK_ARG(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "shape too large");
   QV_CHECK_ARG((uint64_t)N * K < (1ull << 32) && (uint64_t)128 * K < (1ull << 31), "weight too large for 32-bit offsets");
   if (M == 0) return QV_OK;
-  QV_CHECK_ARG(a && b && out && (mode == 2 || (ws && as)) && (mode != 1 || bias), "null pointer argument");
+  QV_CHECK_ARG(a && b && out && (mode == 2 || (ws && as)) && ((mode != 1 && mode != 3) || bias) &&
+                   (mode != 3 || gamma),
+               "null pointer argument");
   QV_CHECK_ARG(((uintptr_t)a % 16) == 0 && ((uintptr_t)b % 16) == 0, "a and b must be 16-byte aligned");
   QV_CHECK_ARG(((uintptr_t)out % 16) == 0, "out must be 16-byte aligned");
   QV_CHECK_ARG(mode == 2 || ((uintptr_t)ws % 8) == 0, "wscales must be 8-byte aligned");
-  QV_CHECK_ARG(mode != 1 || ((uintptr_t)bias % 8) == 0, "bias must be 8-byte aligned");
+  QV_CHECK_ARG((mode != 1 && mode != 3) || ((uintptr_t)bias % 8) == 0, "bias must be 8-byte aligned");
+  QV_CHECK_ARG(mode != 3 || ((uintptr_t)gamma % 16) == 0, "gamma must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   const long big_tiles = (long)((M + 127) / 128) * ((N + 255) / 256);
   const bool big = big_tiles >= 256;
-#define QV_W8(MT)                                                                        \
-  switch (mode) {                                                                        \
-    case 0: launch<MT, 0>(a, b, ws, as, bias, out, (int)M, (int)N, (int)K, st); break;   \
-    case 1: launch<MT, 1>(a, b, ws, as, bias, out, (int)M, (int)N, (int)K, st); break;   \
-    default: launch<MT, 2>(a, b, ws, as, bias, out, (int)M, (int)N, (int)K, st); break;  \
+#define QV_W8(MT)                                                                               \
+  switch (mode) {                                                                               \
+    case 0: launch<MT, 0>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;   \
+    case 1: launch<MT, 1>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;   \
+    case 3: launch<MT, 3>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;   \
+    default: launch<MT, 2>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;  \
   }
   if (big) {
     QV_W8(4)
@@ -319,10 +336,16 @@ static int w8a8_run(const void* a, const void* b, const void* ws, const void* as
 
 extern "C" int qv_w8a8_gemm(const int8_t* a, const int8_t* b, const void* wscales, const void* ascales,
                             const void* bias, void* out, int64_t M, int64_t N, int64_t K, void* stream) {
-  return qv::w8a8_run(a, b, wscales, ascales, bias, out, M, N, K, bias ? 1 : 0, stream);
+  return qv::w8a8_run(a, b, wscales, ascales, bias, nullptr, out, M, N, K, bias ? 1 : 0, stream);
+}
+
+extern "C" int qv_w8a8_gemm_residual(const int8_t* a, const int8_t* b, const void* wscales, const void* ascales,
+                                     const void* bias, const void* gamma, void* residual, int64_t M, int64_t N,
+                                     int64_t K, void* stream) {
+  return qv::w8a8_run(a, b, wscales, ascales, bias, gamma, residual, M, N, K, 3, stream);
 }
 
 extern "C" int qv_w8a8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* out, int64_t M, int64_t N, int64_t K,
                                 void* stream) {
-  return qv::w8a8_run(a, b, nullptr, nullptr, nullptr, out, M, N, K, 2, stream);
+  return qv::w8a8_run(a, b, nullptr, nullptr, nullptr, nullptr, out, M, N, K, 2, stream);
 }

@@ -1,12 +1,20 @@
-"""VGGT aggregator on the GPU: block-level parity against the fp32 oracle
+"""VGGT aggregator on the GPU: block-level parity against the oracle
 (oracle/aggregator.py) at the benchmark shapes, and wiring / determinism of
 the full aggregator.
 
 Blocks are compared through their residual update (x_out - x_in) with
 LayerScale set to 1, so the attention and MLP outputs dominate the check
-instead of the residual stream.  Tolerance: max|d - d_ref| / max|d_ref| <=
-1e-2 for W4A16 (fp32-dequantised reference), 3e-2 for W8A8 (int8 activation
-quantisation of the GPU's fp16 intermediates vs the fp32 reference's).
+instead of the residual stream.  max|d - d_ref| / max|d_ref|:
+
+* W4A16 against the fp32-dequantised reference: <= 1e-2.
+* W8A8 against the reference's W8A8 op chain (every quantiser fed the fp16
+  tensor the previous op stores), in stages: the attention output (the
+  chain's one op that is not bit-exact) <= 1e-2; everything after it
+  (invoke_quant, proj, residual, LN + quant, fc1, GELU + quant, fc2,
+  residual), run teacher-forced from the GPU's own fp16 attention output,
+  bit for bit; end to end <= 2e-2, because an fp16 attention value one
+  rounding away from the oracle's can move an int8 code of invoke_quant by
+  one step (measured 1.07e-2 at S = 8 with attention at 4.5e-4).
 """
 import numpy as np
 import pytest
@@ -38,12 +46,24 @@ def _block_case(gpu, S, seq_len, w8a8, n_rows, seed, tol):
     blk(x, seq_len if seq_len else M, pos, tables, ws)
     torch.cuda.synchronize()
     rows = np.sort(np.random.default_rng(seed + 1).choice(M, n_rows, replace=False))
-    got = x.float().cpu().numpy()[rows] - x0.astype(np.float32)[rows]
+    got = x.float().cpu().numpy()[rows].astype(np.float64) - x0.astype(np.float64)[rows]   # exact
+    att_gpu = ws["att"].cpu().numpy()[rows]          # the block's attention output, fp16
     c, s = R.rope2d_tables(38)
-    ref = OA.aa_block_delta(x0, _params(blk), seq_len if seq_len else M, pos.cpu().numpy(), c, s, rows,
-                            w8a8=w8a8)
+    prm = _params(blk)
+    att = {}
+    o = OA.aa_block_attention(x0, prm, seq_len if seq_len else M, pos.cpu().numpy(), c, s, rows, w8a8=w8a8,
+                              att_out=att)
+    ref = OA.aa_block_finish(x0[rows], o, prm, w8a8=w8a8)
+    err_att = np.abs(att_gpu.astype(np.float64) - att["att"]).max() / np.abs(att["att"]).max()
     err = np.abs(got - ref).max() / np.abs(ref).max()
-    assert np.isfinite(got).all() and err <= tol, err
+    msg = f"attention {err_att:.2e}, block {err:.2e}"
+    if w8a8:
+        tf = OA.w8a8_block_from_attention(x0[rows], att_gpu, prm)
+        err_tf = np.abs(got - tf).max() / np.abs(tf).max()
+        msg += f", from the GPU attention on {err_tf:.2e}"
+        assert np.array_equal(got, tf), msg        # bit-exact ops from here on
+    print(f"[block] S={S} {'w8a8' if w8a8 else 'w4a16'}: {msg}", flush=True)
+    assert np.isfinite(got).all() and err_att <= 1e-2 and err <= tol, msg
     return err
 
 
@@ -58,7 +78,7 @@ def test_global_block_w4_s32(gpu):
 
 
 def test_frame_block_w8a8_s8(gpu):
-    _block_case(gpu, S=8, seq_len=1374, w8a8=True, n_rows=128, seed=2, tol=3e-2)
+    _block_case(gpu, S=8, seq_len=1374, w8a8=True, n_rows=128, seed=2, tol=2e-2)
 
 
 def test_aggregator_wiring_and_determinism(gpu):

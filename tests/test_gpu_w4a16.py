@@ -402,6 +402,39 @@ def test_skinny_split_k_bf16(gpu):
     assert O.rel_err(y.float().cpu().numpy(), O.bf16_bits_to_f32(xb) @ W.T) <= TOL
 
 
+def test_skinny_split_k_captured_on_a_fresh_stream_matches_eager(gpu):
+    """A split-K skinny call captured into a graph on a stream the library has
+    never run on takes the same split plan as an eager call (it uses the
+    device scratch, since capture cannot allocate), so every replay equals
+    the eager output bit for bit; eager calls on the capture stream and on
+    the current stream run between the replays.  One eager call comes first:
+    a device's first split-K call sets the device scratch up, outside
+    capture."""
+    from qvggt_amd import awq_inference_engine as E
+    M, N, K = 32, 2048, 8192
+    p = O.make_w4_problem(M, K, N, seed=77)
+    t = _to_dev(p, gpu)
+    out = torch.empty(M, N, dtype=torch.float16, device=gpu)
+    E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], out=out)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], out=out)
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    for i in range(3):
+        t["x"].copy_(torch.randn(M, K, generator=gen, device=gpu).half())
+        want = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"])
+        with torch.cuda.stream(s):
+            other = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"])
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want) and torch.equal(other, want), i
+    W = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K)
+    assert O.rel_err(out.float().cpu().numpy(), O.gemm_ref(t["x"].cpu().numpy(), W)) <= TOL
+
+
 @pytest.mark.parametrize("M", [1374, 2748, 300, 40])
 def test_qkv_qknorm_rope_fused_matches_two_step(gpu, M):
     """qv_w4a16_gemm_qkrope (the qkv projection with its q/k LayerNorm and 2-D

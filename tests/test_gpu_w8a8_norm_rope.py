@@ -99,6 +99,30 @@ def test_w8a8_gemm_fp16_bit_exact(gpu, M, N, K, bias):
     assert np.array_equal(_bits(out), ref.view(np.int16))
 
 
+@pytest.mark.parametrize("M,N,K", [(10992, 1024, 4096), (1374, 1024, 1024), (129, 1040, 1024)])
+def test_w8a8_linear_residual_bit_exact(gpu, M, N, K):
+    """qv_w8a8_gemm_residual: residual = fp16(residual + gamma * o), o the bit-exact
+    fp16 epilogue of the GEMM with bias; o * gamma is exact in fp32, so the
+    result is one rounding of residual + o * gamma.  The 10992 x 4096 -> 1024
+    shape takes 128-row tiles (epilogue operands prefetched), the others
+    64-row tiles; N = 1040 leaves a partial column tile."""
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(M * 7 + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    a, as_ = Q.quant_per_token(x)
+    b = np.clip(np.rint(rng.standard_normal((N, K)) * 32), -128, 127).astype(np.int8)
+    ws = rng.uniform(0.0005, 0.005, N).astype(np.float16)
+    bb = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    g = rng.uniform(0.005, 1.5, N).astype(np.float16)
+    r0 = rng.standard_normal((M, N)).astype(np.float16)
+    resid = torch.from_numpy(r0).to(gpu)
+    t = [torch.from_numpy(v).to(gpu) for v in (a, b, ws, as_, bb, g)]
+    E.w8a8_linear_residual(*t, resid)
+    o = Q.w8a8_epilogue(Q.w8a8_int32(a, b), ws, as_, bb)
+    ref = (r0.astype(np.float32) + o.astype(np.float32) * g.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(_bits(resid), ref.view(np.int16))
+
+
 # ------------------------------------------------------- LN + quant
 @pytest.mark.parametrize("M,D,dt", [(10992, 1024, "f16"), (33, 4096, "f16"), (7, 1000, "f16"), (1001, 2048, "f16"), (18, 512, "f16"),
                                     (1374, 1024, "bf16"), (65, 4096, "bf16"), (300, 1024, "f32"), (9, 2048, "f32")])
@@ -272,15 +296,20 @@ def test_vggt_layer_norm_bit_exact(gpu, M):
 
 
 # ------------------------------------------------------------------ RoPE
-@pytest.mark.parametrize("transpose_out", [False, True])
 @pytest.mark.parametrize("dt", [torch.float16, torch.float32, torch.bfloat16])
-def test_fused_rope_with_pos(gpu, transpose_out, dt):
+@pytest.mark.parametrize("transpose_out", [False, True])
+@pytest.mark.parametrize("shape", [(37, 3, 16, 64, 48), (5, 2, 3, 40, 20), (3, 1, 2, 1040, 1032), (2, 2, 1, 1040, 1024)],
+                         ids=["vec", "elementwise", "wide_elementwise", "wide_vec"])
+def test_fused_rope_with_pos(gpu, transpose_out, dt, shape):
     """fused_rope_with_pos.cu:155-161 dispatches float, half and bfloat16.
     fp16 / bf16 within one ulp of the oracle's rounding (and equal in more
-    than 99.9 % of elements), fp32 within 2e-6 relative."""
+    than 99.9 % of elements), fp32 within 2e-6 relative.  The shapes take the
+    kernel's paths: 16-byte chunks (d2/2 and d - d2 multiples of 8), element
+    accesses (d2/2 = 10; d2/2 = 516), and d2 > 512, where the cos / sin of
+    the angles are evaluated per element instead of once per position."""
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(3)
-    S, B, H, D, D2 = 37, 3, 16, 64, 48
+    S, B, H, D, D2 = shape
     base = rng.standard_normal((B, S, H, D)).astype(np.float32)
     freqs = rng.uniform(-20, 20, (B, S, D2)).astype(np.float32)
     xt = torch.from_numpy(base).to(gpu).to(dt).transpose(0, 1)   # (S,B,H,D), non-contiguous

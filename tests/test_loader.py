@@ -154,3 +154,19 @@ def test_model_config_is_read_like_the_reference(tmp_path):
     assert LD.load_model_config(qdir / "model.safetensors", mdir / "w.pt").block_ln_eps == 3e-6
     with pytest.raises(ValueError, match="unsupported"):
         AggregatorConfig.from_dict({"hidden_size": 768})
+
+
+def test_model_config_sections_do_not_override_each_other():
+    """A patch_embed_config section sets only the DINOv2 fields (its plain
+    depth / layer_norm_eps included); the aggregator section's values set the
+    AA blocks, whichever order the sections appear in."""
+    from qvggt_amd.aggregator import AggregatorConfig
+    d = {"aggregator_config": {"layer_norm_eps": 1e-5, "depth": 24},
+         "patch_embed_config": {"layer_norm_eps": 1e-6, "depth": 12}}
+    for cfg in (d, dict(reversed(list(d.items())))):
+        c = AggregatorConfig.from_dict(cfg)
+        assert (c.depth, c.block_ln_eps, c.dino_depth, c.dino_ln_eps) == (24, 1e-5, 12, 1e-6)
+    c = AggregatorConfig.from_dict({"patch_embed_config": {"norm_eps": 1e-5}})
+    assert (c.block_ln_eps, c.dino_ln_eps, c.depth) == (1e-6, 1e-5, 24)
+    c = AggregatorConfig.from_dict({"aa_depth": 8, "patch_embed_depth": 6, "layer_norm_eps": 1e-5})
+    assert (c.depth, c.dino_depth, c.block_ln_eps, c.dino_ln_eps) == (8, 6, 1e-5, 1e-6)

@@ -334,3 +334,76 @@ def test_qknorm_rope2d_is_float64_layernorm_then_complex_rotation():
         assert np.abs(y[..., 32 * half + 16:32 * half + 32] - r.imag).max() < tol
     # specials (position 0) are the bare fp16 LayerNorm
     assert np.abs(y[:5] - ln[:5]).max() < 2e-3 * np.abs(ln).max()
+
+
+def _rne(q, mant_bits: int, emin: int):
+    """Round the rational q to the nearest binary float with ``mant_bits``
+    fraction bits and minimum normal exponent ``emin`` (ties to even,
+    subnormals below 2**emin, no overflow handling needed here), exactly."""
+    from fractions import Fraction
+    if q == 0:
+        return Fraction(0)
+    sign = -1 if q < 0 else 1
+    a = abs(Fraction(q))
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    ulp = Fraction(2) ** (max(e, emin) - mant_bits)
+    n, r = divmod(a, ulp)
+    if r > ulp / 2 or (r == ulp / 2 and n % 2 == 1):
+        n += 1
+    return sign * n * ulp
+
+
+def test_gelu_fast_f16_rounding_order_known_answers():
+    """act.cu:22-28 with T = half fixes the order and the rounding of every
+    operation: a = h(f * c1), b = h(h(c2 * f) * x), c = h(1 + b), u = h(a * c),
+    t = h(fp32(tanh u)), y = h(h(0.5 * x) * h(1 + t)), h = round to fp16.
+    Restated here in exact rational arithmetic with its own round-to-nearest-
+    even (not numpy's float16), over every 3rd fp16 value in [-8, 8].  The
+    inputs are also evaluated with three plausible mistakes -- one rounding at
+    the end, the product reassociated as c2 * h(f * x), and 1 + b left
+    unrounded inside u -- each of which must disagree with the reference order
+    somewhere, so the oracle's agreement pins its order."""
+    import math
+    from fractions import Fraction as Fr
+    h = lambda q: _rne(q, 10, -14)
+    f32 = lambda q: _rne(q, 23, -126)
+    bits = np.arange(0x8000, dtype=np.uint32).astype(np.uint16)
+    vals = np.concatenate([bits.view(np.float16), (bits | 0x8000).view(np.float16)])
+    vals = vals[np.isfinite(vals) & (np.abs(vals.astype(np.float64)) <= 8)][::3]
+    c1, c2 = Fr(float(np.float16(0.79788456))), Fr(float(np.float16(0.044715)))
+    half, one = Fr(1, 2), Fr(1)
+
+    def tanh16(u):
+        return h(f32(Fr(math.tanh(float(u)))))
+
+    def ref(x):
+        a = h(x * c1)
+        b = h(h(c2 * x) * x)
+        u = h(a * h(one + b))
+        return h(h(half * x) * h(one + tanh16(u)))
+
+    def one_rounding(x):
+        u = x * c1 * (one + c2 * x * x)
+        return h(half * x * (one + Fr(math.tanh(float(u)))))
+
+    def reassoc(x):
+        a = h(x * c1)
+        b = h(c2 * h(x * x))
+        u = h(a * h(one + b))
+        return h(h(half * x) * h(one + tanh16(u)))
+
+    def unrounded_sum(x):
+        a = h(x * c1)
+        b = h(h(c2 * x) * x)
+        u = h(a * (one + b))
+        return h(h(half * x) * h(one + tanh16(u)))
+
+    xs = [Fr(float(v)) for v in vals]
+    want = np.array([float(ref(x)) for x in xs])
+    got = Q.gelu_fast_f16(vals).astype(np.float64)
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:10]
+    for alt in (one_rounding, reassoc, unrounded_sum):
+        other = np.array([float(alt(x)) for x in xs])
+        assert (other != want).any(), alt.__name__
