@@ -92,7 +92,6 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
       zv[j] = __builtin_amdgcn_raw_buffer_load_b16(rsZ, sz_voff[j], (ks >> 1) * N * 2, 0);
     }
   };
-  constexpr int B_INSTR = 3 * NT;               // VMEM instructions of one load_b
 
   const uint32_t lds0 = lds_addr(lds);
   auto issue = [&](int ks, int st) {
@@ -117,80 +116,90 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
       }
     }
   };
-  // One stage: k-step s issues the LDS reads of step s+1's activations, then
-  // its own MFMAs, then dequantises step s+1's weights (VALU that co-issues
-  // with the MFMAs in flight).  The scheduling fences keep the compiler from
-  // sinking the reads next to their use, which would expose LDS latency.
-  auto compute = [&](int st, const uint4 (&wq)[NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT]) {
+  // activation fragments of k-step s of the stage in LDS buffer st
+  auto read_a = [&](int st, int s, uint4 (&af)[MT]) {
     const uint8_t* base = lds + st * STAGE;
+    const uint32_t col = (uint32_t)(((4 * h + s) ^ fa) * 16);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) af[i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 128 + col);
+  };
+  // One stage (LDS buffer st, weights wq/sv/zv).  On entry af0 / wf0 hold the
+  // stage's k-step 0 fragments; k-step s issues the LDS reads of step s+1's
+  // activations, then its own MFMAs, then dequantises step s+1's weights
+  // (VALU that co-issues with the MFMAs in flight).  Step 3 does the same for
+  // k-step 0 of the NEXT stage (buffer nst, weights nwq/nsv/nzv), so the next
+  // stage's first MFMAs do not wait behind its barrier for LDS reads and a
+  // dequantisation; af0 / wf0 hold those fragments on exit.  The scheduling
+  // fences keep the compiler from sinking the reads next to their use.
+  auto compute = [&](int st, int nst, const uint4 (&wq)[NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT],
+                     const uint4 (&nwq)[NT], const uint32_t (&nsv)[NT], const uint32_t (&nzv)[NT], uint4 (&af0)[MT],
+                     uint4 (&wf0)[NT]) {
     uint4 af[2][MT], wf[2][NT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
-      af[0][i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 128 + (uint32_t)(((4 * h) ^ fa) * 16));
-    dq(0, wq, sv, zv, wf[0]);
+    for (int i = 0; i < MT; ++i) af[0][i] = af0[i];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) wf[0][j] = wf0[j];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      if (s < 3) {
-        const uint32_t col = (uint32_t)(((4 * h + s + 1) ^ fa) * 16);
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-          af[(s + 1) & 1][i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 128 + col);
-      }
+      if (s < 3) read_a(st, s + 1, af[(s + 1) & 1]);
+      else read_a(nst, 0, af[0]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[j][i] = mfma32<BF16>(wf[s & 1][j], af[s & 1][i], acc[j][i]);
       }
-      if (s < 3) dq(s + 1, wq, sv, zv, wf[(s + 1) & 1]);
+      if (s < 3) {
+        dq(s + 1, wq, sv, zv, wf[(s + 1) & 1]);
+      } else {
+        // the next stage's weights (and every copy issued before them) have landed
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        dq(0, nwq, nsv, nzv, wf[0]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) af0[i] = af[0][i];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) wf0[j] = wf[0][j];
   };
 
-  // Per stage ks: barrier, B(ks+1) into the idle register set, b_wait, then
-  // A(ks+2), then compute stage ks.  b_wait = vmcnt(B_INSTR) lands everything
-  // issued before B(ks+1): B(ks) and A(ks+1), so the next barrier publishes
-  // every wave's A(ks+1).  The A copies are inline asm the compiler does not
-  // count; waiting right after B(ks+1) is the one place where the hardware
-  // count and the compiler's own count agree that B(ks) is done, so the
-  // compiler adds no wait of its own before stage ks's MFMAs (a wait placed
-  // after A(ks+2) would make it wait, by its count, for loads just issued).
-  // top_wait's vmcnt(A_INSTR + B_INSTR) is a no-op in this order; it keeps
-  // A(ks+1) landed before the barrier however the compiler places the
-  // register loads within a stage.  Past the last stage the loads repeat
-  // stage KS-1 (valid addresses; A into a buffer nobody reads any more, B
-  // into a dead register set), so every iteration issues the same count.
-  static_assert(A_INSTR + B_INSTR < 16, "the vmcnt immediates use the low 4 bits only");
-  auto b_wait = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70 | B_INSTR); };
-  auto top_wait = [&]() {
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (A_INSTR + B_INSTR));
-    lds_barrier();
-  };
-  // B registers alternate between two sets (stage i = ks - k0 uses set i & 1
-  // and LDS buffer i % 3); k0 and k1 are even (whole 128-k groups), so every
-  // iteration runs two stages.  Loads past k1 - 1 repeat stage k1 - 1.  (An
-  // odd stage count, with a conditional second half, made the compiler
-  // spill the accumulators in a kernel that loops over tiles.)
+  // Stage i = ks - k0 uses LDS buffer i % 3 and weight register set i & 1.
+  // Per stage: barrier (every wave is done reading buffer (i + 2) % 3, the
+  // previous stage's, and sees A(ks + 1)), the copy of A(ks + 2) into that
+  // buffer, the weight loads B(ks + 1) into the idle register set, then the
+  // stage's compute, whose last step waits for all of this wave's loads
+  // (vmcnt(0): A(ks + 2) was issued before B(ks + 1), so it is no extra wait)
+  // and reads stage ks + 1's first fragments -- A(ks + 1) landed at the same
+  // point of the previous stage, before the barrier that published it.  The
+  // A copies are inline asm the compiler does not count; the compiler's own
+  // wait for B(ks + 1) is that same vmcnt(0).  k0 and k1 are even (whole
+  // 128-k groups), so every iteration runs two stages.  Loads past k1 - 1
+  // repeat stage k1 - 1 (valid addresses; A into a buffer nobody reads, B into
+  // a dead register set), so every stage issues the same count.  (An odd
+  // stage count, with a conditional second half, made the compiler spill the
+  // accumulators in a kernel that loops over tiles.)
   uint4 wq0[NT], wq1[NT];
   uint32_t sv0[NT], zv0[NT], sv1[NT], zv1[NT];
+  uint4 af0[MT], wf0[NT];
   const int last = k1 - 1, nks = k1 - k0;
   issue(k0, 0);
+  issue(k0 + 1 < k1 ? k0 + 1 : last, 1);
   load_b(k0, wq0, sv0, zv0);
-  issue(k0 + 1, 1);
-  // lands A(0) wherever the compiler places B(0) relative to A(1)
-  __builtin_amdgcn_s_waitcnt(0x0F70 | A_INSTR);
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): A(k0), A(k0 + 1), B(k0)
+  lds_barrier();
+  read_a(0, 0, af0);
+  dq(0, wq0, sv0, zv0, wf0);
   for (int i = 0; i < nks; i += 2) {
     const int ks = k0 + i;
-    top_wait();
-    load_b(ks + 1, wq1, sv1, zv1);
-    b_wait();
+    lds_barrier();
     issue(ks + 2 < k1 ? ks + 2 : last, (i + 2) % NSTAGE);
-    compute(i % NSTAGE, wq0, sv0, zv0);
-    top_wait();
-    load_b(ks + 2 < k1 ? ks + 2 : last, wq0, sv0, zv0);
-    b_wait();
+    load_b(ks + 1, wq1, sv1, zv1);
+    compute(i % NSTAGE, (i + 1) % NSTAGE, wq0, sv0, zv0, wq1, sv1, zv1, af0, wf0);
+    lds_barrier();
     issue(ks + 3 < k1 ? ks + 3 : last, (i + 3) % NSTAGE);
-    compute((i + 1) % NSTAGE, wq1, sv1, zv1);
+    load_b(ks + 2 < k1 ? ks + 2 : last, wq0, sv0, zv0);
+    compute((i + 1) % NSTAGE, (i + 2) % NSTAGE, wq1, sv1, zv1, wq0, sv0, zv0, af0, wf0);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the repeated loads may not land during the epilogue
 }

@@ -43,7 +43,6 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
   constexpr int NSTAGE = 3;
   constexpr int A_INSTR = BM / 64;   // 1 KB direct loads per wave per stage (A)
   constexpr int B_INSTR = 4;         // 16 KB / 1 KB / 4 waves
-  constexpr int VM_PER_STAGE = A_INSTR + B_INSTR;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * STAGE];
 
   const int tid = threadIdx.x;
@@ -126,43 +125,62 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0;
 
   const int fl = f8(l32);  // f has period 16: f(32*i + l32) == f(l32), and f(64*w + 32*j + l32) too
-  // Both k-steps' fragments are read up front (6 x b128 each), the second
-  // step's reads in flight while the first step's MFMAs issue; the fence keeps
-  // the compiler from sinking them next to their use.
-  auto compute = [&](int st) {
+  // Fragments of k-step s of the stage in LDS buffer st (weights, activations).
+  auto read = [&](int st, int s, uint4 (&bw)[NT], uint4 (&av)[MT]) {
     const uint8_t* base = lds + st * STAGE;
-    uint4 bw[2][NT], av[2][MT];
+    const uint32_t col = (uint32_t)(((2 * s + h) ^ fl) * 16);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const uint32_t col = (uint32_t)(((2 * s + h) ^ fl) * 16);
+    for (int j = 0; j < NT; ++j)
+      bw[j] = *reinterpret_cast<const uint4*>(base + A_BYTES + (64 * wave + 32 * j + l32) * 64 + col);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) av[i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 64 + col);
+  };
+  auto mfmas = [&](const uint4 (&bw)[NT], const uint4 (&av)[MT]) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int j = 0; j < NT; ++j)
-        bw[s][j] = *reinterpret_cast<const uint4*>(base + A_BYTES + (64 * wave + 32 * j + l32) * 64 + col);
-#pragma unroll
-      for (int i = 0; i < MT; ++i) av[s][i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 64 + col);
-    }
+        acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bw[j]),
+                                                          __builtin_bit_cast(i32x4, av[i]), acc[j][i], 0, 0, 0);
+  };
+  // One stage (buffer st).  On entry b0 / a0 hold its k-step 0 fragments.
+  // Step 0 issues the reads of step 1, then its MFMAs; step 1 issues the
+  // reads of the NEXT stage's k-step 0 (buffer nst), then its MFMAs, so no
+  // stage starts with its MFMAs waiting behind the barrier for LDS reads.
+  // The fences keep the compiler from sinking each read next to its use.
+  uint4 b0[NT], a0[MT];
+  auto compute = [&](int st, int nst) {
+    uint4 b1[NT], a1[MT];
+    read(st, 1, b1, a1);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bw[s][j]),
-                                                            __builtin_bit_cast(i32x4, av[s][i]), acc[j][i], 0, 0, 0);
+    mfmas(b0, a0);
+    __builtin_amdgcn_sched_barrier(0);
+    read(nst, 0, b0, a0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(b1, a1);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
+  // Stage ks uses buffer ks % 3.  At its top: vmcnt(0) lands this wave's
+  // copies of stage ks + 1 (issued one stage earlier), and the barrier makes
+  // every wave's visible and guarantees every wave is done with buffer
+  // (ks + 2) % 3 = the previous stage's, which then receives stage ks + 2.
+  // Stages past KS - 1 are not copied; the last stage's read of the "next"
+  // stage reads a buffer nobody uses again (its values are dropped).
   issue(0, 0);
   if (KS > 1) issue(1, 1);
+  // vmcnt(0): stages 0 and 1; lgkmcnt(0), as a builtin the compiler sees:
+  // a scalar load it hoisted here (a kernel argument of the epilogue) would
+  // otherwise count as pending through the loop, and since scalar loads
+  // return out of order the compiler would wait lgkmcnt(0) for every LDS read
+  __builtin_amdgcn_s_waitcnt(0x0070);
+  lds_barrier();
+  read(0, 0, b0, a0);
   for (int ks = 0; ks < KS; ++ks) {
-    if (ks + 1 < KS) {
-      __builtin_amdgcn_s_waitcnt(0x0F70 | VM_PER_STAGE);  // vmcnt(VM_PER_STAGE)
-    } else {
-      __builtin_amdgcn_s_waitcnt(0x0F70);                 // vmcnt(0)
-    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     lds_barrier();
     if (ks + 2 < KS) issue(ks + 2, (ks + 2) % NSTAGE);
-    compute(ks % NSTAGE);
+    compute(ks % NSTAGE, (ks + 1) % NSTAGE);
   }
 
   if constexpr (OUT == 2) {

@@ -27,8 +27,9 @@ same shapes, for scale: an unquantised fp16 ``torch.mm`` / ``torch.addmm``
 (hipBLASLt), an int8 x int8 -> int32 ``torch._int_mm`` (hipBLASLt, the W8A8
 counterpart) and torch's ``scaled_dot_product_attention``, each replayed
 from a HIP graph after a 1 s warm-up.  ``rows`` runs each HBM-bound row
-kernel at its benchmark shape -- LayerNorm, per-token quant and LN + quant on
-S = 32 tokens (43968 x 1024), GELU + quant on the MLP hidden (10992 x 4096),
+kernel at its benchmark shape -- LayerNorm, per-token quant, LN + quant, T5
+RMSNorm and rotate-half RoPE (fused_rope_with_pos, 16 heads of 64 with fp32
+angles) on S = 32 tokens (43968 x 1024), GELU + quant on the MLP hidden (10992 x 4096),
 2-D RoPE and qk-norm + 2-D RoPE on the S = 32 qkv (43968 x 3072) -- R times,
 each launch on its own buffer set (so no launch finds its data in the
 caches).  ``w8a8`` runs the W8A8 GEMM with bias (int8 MFMA) on random int8
@@ -175,8 +176,13 @@ def _rows(reps):
         E.invoke_quant(q8[i], xs[i], sc[i])
     for i in range(reps):
         E.rms_norm_general(q8[i], xs[i], g, b, sc[i], 1e-6, True)
+    for i in range(reps):
+        E.layernorm_forward_cuda(xs[i].view(32, 1374, D), g, ys[i].view(32, 1374, D), 1e-6)
+    fr = [torch.rand(1, M, 64, device=dev) * 40 - 20 for _ in range(reps)]
+    for i in range(reps):
+        E.fused_rope_with_pos_forward_func(xs[i].view(M, 1, 16, 64), fr[i], False)
     torch.cuda.synchronize()
-    del xs, ys, q8, sc
+    del xs, ys, q8, sc, fr
     Mh, Dh = 8 * 1374, 4096
     for i in range(reps):
         hx = torch.randn(Mh, Dh, **f16)
@@ -195,8 +201,8 @@ def _rows(reps):
     for i in range(reps):
         E.qknorm_rope2d(qkv[i], pos, ct, st, 16, gq, bq, gq, bq)
     torch.cuda.synchronize()
-    print(f"rows: layernorm, quant, ln+quant (S=32), gelu+quant (10992x4096), rope2d, qknorm_rope2d (S=32), "
-          f"{reps} launches each", flush=True)
+    print(f"rows: layernorm, quant, ln+quant, rmsnorm, rope_with_pos (S=32), gelu+quant (10992x4096), rope2d, "
+          f"qknorm_rope2d (S=32), {reps} launches each", flush=True)
 
 
 def _w8a8(M, K, N, reps):

@@ -483,6 +483,46 @@ def test_qkv_qknorm_rope_fused_matches_two_step(gpu, M):
     assert worst <= 3.0, f"q/k heads differ by {worst} fp16 ulp of the head row's largest value"
 
 
+@pytest.mark.parametrize("M", [1374, 2748])
+def test_qkv_qknorm_rope_fused_matches_oracle(gpu, M):
+    """qv_w4a16_gemm_qkrope against the oracle directly: the fp32-dequantised
+    projection plus bias (float64 from the dequantised weights), rounded to
+    fp16 as the epilogue stores it, then oracle.rope.qknorm_rope2d (the
+    reference q/k LayerNorm + 2-D RoPE) on the q and k heads; v heads are the
+    projection itself.  Tolerance: max |out - ref| <= 1e-2 of max |ref| per
+    part, and the q / k values within a few fp16 steps of their head row's
+    largest value (the GEMM's fp32 sum may round y to the neighbouring fp16
+    value, which the LayerNorm and rotation then carry)."""
+    from oracle import rope as R
+    from qvggt_amd import awq_inference_engine as E
+    H, K = 16, 1024
+    N = 3 * H * 64
+    p = O.make_w4_problem(M, K, N, seed=M + 5)
+    t = _to_dev(p, gpu)
+    rng = np.random.default_rng(M + 5)
+    bias = (rng.standard_normal(N) * 0.5).astype(np.float16)
+    pos = R.vggt_positions(M // 1374)
+    ct, st = E.rope2d_tables(38, device=gpu)
+    prm = [((1 if i % 2 == 0 else 0) + 0.1 * rng.standard_normal(64)).astype(np.float16) for i in range(4)]
+    got = E.w4a16_linear_qkrope(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], torch.from_numpy(bias).to(gpu),
+                                torch.from_numpy(pos).to(gpu), ct, st, H, *(torch.from_numpy(v).to(gpu) for v in prm),
+                                eps=1e-6)
+    torch.cuda.synchronize()
+    W = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K).astype(np.float64)
+    y = (p["x"].astype(np.float64) @ W.T + bias.astype(np.float64)).astype(np.float16).reshape(M, 3, H, 64)
+    c, s = R.rope2d_tables(38)
+    qk = R.qknorm_rope2d(y[:, :2], pos, c, s, *prm, eps=1e-6).astype(np.float64)
+    g = got.view(M, 3, H, 64).cpu().numpy().astype(np.float64)
+    for part, ref in ((0, qk[:, 0]), (1, qk[:, 1]), (2, y[:, 2].astype(np.float64))):
+        err = np.abs(g[:, part] - ref).max() / np.abs(ref).max()
+        assert np.isfinite(g[:, part]).all() and err <= 1e-2, (part, err)
+    row_max = np.abs(qk).max(axis=-1, keepdims=True)
+    ulp = np.spacing(row_max.astype(np.float16)).astype(np.float64)
+    worst = (np.abs(g[:, :2] - qk) / ulp).max()
+    print(f"[qkrope] M={M}: max |fused - oracle| = {worst:.2f} ulp of the head row's max", flush=True)
+    assert worst <= 8.0, worst
+
+
 # Shapes whose launch covers the rows in two ranges of different tile heights
 # (the tile planner picks 96- then 64-row tiles for 2748 x 3072, 128- then
 # 96-row tiles for the others), with the epilogue each runs with in the model.
