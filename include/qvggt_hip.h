@@ -206,7 +206,9 @@ int qv_layernorm_quant(const void* x, int dtype, const void* gamma, const void* 
 /*
  * tanh-GELU (fp16 arithmetic) fused with per-token int8 quantisation; tmp
  * receives the fp16 GELU output.  Replaces gelu_and_quant (w8a8/act.h:5-10,
- * act.cu:22-90).
+ * act.cu:22-90).  tmp may be NULL (an extension: the reference always writes
+ * it, as the scratch its kernel re-reads): q and scale are the same, and the
+ * 2 bytes per element of tmp are not written.
  */
 int qv_gelu_quant(const void* x, int8_t* q, void* scale, void* tmp, int64_t M, int64_t D,
                   void* stream);

@@ -328,7 +328,7 @@ class AABlock(nn.Module):
         else:
             E.rms_norm_general(ws["q8"], x, self.norm2.weight, self.norm2.bias, ws["s8"], eps, True)
             f = m.fc1(ws["q8"], ws["s8"], out=ws["f"])
-            E.gelu_and_quant(ws["q8f"], f, ws["s8"], ws["ftmp"])
+            E.gelu_and_quant(ws["q8f"], f, ws["s8"], None)   # the fp16 GELU copy is not needed
             m.fc2.forward_residual(ws["q8f"], ws["s8"], self.ls2.gamma, x)
         return x
 
@@ -527,7 +527,7 @@ class Aggregator(nn.Module):
                 self._ws.update({
                     "q8": torch.empty(M, DIM, dtype=torch.int8, device=dev),
                     "q8f": torch.empty(M, MLP_DIM, dtype=torch.int8, device=dev),
-                    "s8": torch.empty(M, **f16), "ftmp": torch.empty(M, MLP_DIM, **f16),
+                    "s8": torch.empty(M, **f16),
                 })
         return self._ws
 

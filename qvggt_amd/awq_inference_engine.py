@@ -507,18 +507,20 @@ def rms_norm_general(out: torch.Tensor, input: torch.Tensor, weight: torch.Tenso
                   C.c_float(epsilon), 1 if use_per_token_quant else 0, M, D, _stream(dev))
 
 
-def gelu_and_quant(out: torch.Tensor, input: torch.Tensor, scale_out: torch.Tensor, tmp: torch.Tensor) -> None:
+def gelu_and_quant(out: torch.Tensor, input: torch.Tensor, scale_out: torch.Tensor, tmp: torch.Tensor | None) -> None:
     """tanh-GELU (fp16 arithmetic) + per-token int8 (w8a8/act.cu:30-90); tmp gets the
-    fp16 GELU values, scale_out the per-token fp16 scales."""
+    fp16 GELU values, scale_out the per-token fp16 scales.  ``tmp=None`` (an
+    extension of the reference op, which always writes it) skips that store."""
     what = "gelu_and_quant"
     if input.dtype != torch.float16:
         _fail(f"{what}: input must be float16 (the reference kernel is half-only)")
     _need(out, torch.int8, what, "out")
     _need(scale_out, torch.float16, what, "scale_out")
-    _need(tmp, torch.float16, what, "tmp")
+    if tmp is not None:
+        _need(tmp, torch.float16, what, "tmp")
     D = input.shape[-1]
     M = input.numel() // D if D else 0
-    if out.numel() != input.numel() or tmp.numel() != input.numel() or scale_out.numel() < M:
+    if out.numel() != input.numel() or (tmp is not None and tmp.numel() != input.numel()) or scale_out.numel() < M:
         _fail(f"{what}: out/tmp must match input, scale_out hold {M} tokens")
     dev = _on_gpu(out, input, scale_out, tmp, what=what)
     x = _contig(input)

@@ -234,7 +234,8 @@ def _trace_summary(path, match, grid, run, last):
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
 
     def hit(r):
-        return match in r["Kernel_Name"] and (grid is None or int(r["Grid_Size"]) == grid)
+        g = r.get("Grid_Size", r.get("Grid_Size_X"))   # rocprofv3 names it Grid_Size_X in newer releases
+        return match in r["Kernel_Name"] and (grid is None or int(g) == grid)
 
     if run:
         first = next(i for i, r in enumerate(rows) if run in r["Kernel_Name"])

@@ -196,6 +196,11 @@ def test_gelu_and_quant_bit_exact(gpu, M, D):
     assert np.array_equal(_bits(tmp), tr.view(np.int16))
     assert np.array_equal(_bits(s), sr.view(np.int16))
     assert np.array_equal(q.cpu().numpy(), qr)
+    # tmp = None (no fp16 copy stored): the same codes and scales
+    q2 = torch.zeros_like(q)
+    s2 = torch.zeros_like(s)
+    E.gelu_and_quant(q2, torch.from_numpy(x).to(gpu), s2, None)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
 
 
 def test_gelu_every_finite_fp16_input(gpu):
