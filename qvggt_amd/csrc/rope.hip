@@ -50,6 +50,39 @@ __device__ __forceinline__ void ld8(const void* p, long e, float (&v)[8]) {
     }
   }
 }
+// The same eight elements as raw 16-byte words (one for 16-bit types, two for
+// fp32), converted later with cvt8: a load whose use comes much later.
+template <int DT>
+struct Raw8 {
+  uint4 w[DT == QV_F32 ? 2 : 1];
+};
+template <int DT>
+__device__ __forceinline__ Raw8<DT> ld8_raw(const void* p, long e) {
+  Raw8<DT> r;
+  if constexpr (DT == QV_F32) {
+    r.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p) + e);
+    r.w[1] = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(p) + e + 4);
+  } else {
+    r.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + e);
+  }
+  return r;
+}
+template <int DT>
+__device__ __forceinline__ void cvt8(const Raw8<DT>& r, float (&v)[8]) {
+  if constexpr (DT == QV_F32) {
+    const uint32_t w[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_bit_cast(float, w[i]);
+  } else {
+    const uint32_t w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = to_f32((uint16_t)(w[i] & 0xFFFF), DT == QV_BF16);
+      v[2 * i + 1] = to_f32((uint16_t)(w[i] >> 16), DT == QV_BF16);
+    }
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ void st8(void* p, long e, const float (&v)[8]) {
   if constexpr (DT == QV_F32) {
@@ -73,29 +106,58 @@ __device__ __forceinline__ void st8(void* p, long e, const float (&v)[8]) {
 // rows, d2/2 and d - d2 multiples of 8): a lane moves 8 dims of the first
 // half and their 8 partners of the second half with 16-byte accesses, then
 // the pass-through dims in 8-element chunks; otherwise a lane takes one
-// (head, pair) at a time with element accesses.  d2 above RWP_MAX_D2 skips
-// the table and evaluates cos / sin per element.
+// (head, pair) at a time with element accesses.  The angles and a lane's
+// first 16-byte pair are loaded before the table is evaluated, so their
+// latency runs under the fp64 cos / sin (with VGGT's 16 heads of 64, d2 = 64,
+// that first pair is all a lane moves).  d2 above RWP_MAX_D2 skips the table
+// and evaluates cos / sin per element.
 constexpr int RWP_WAVES = 4;
 constexpr int RWP_MAX_D2 = 512;
 
-template <int DT, bool VEC>
+template <int DT, bool VEC, bool TAB>
 __global__ __launch_bounds__(64 * RWP_WAVES) void rope_with_pos_kernel(
     const void* __restrict__ x, const float* __restrict__ freqs, void* __restrict__ out, int S, int B, int H,
     int D, int D2, long sx_s, long sx_b, long sx_h, long sx_d, long so_s, long so_b, long so_h, long so_d) {
-  __shared__ float cs_l[RWP_WAVES][RWP_MAX_D2], sn_l[RWP_WAVES][RWP_MAX_D2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float cs_l[TAB ? RWP_WAVES : 1][TAB ? RWP_MAX_D2 : 1], sn_l[TAB ? RWP_WAVES : 1][TAB ? RWP_MAX_D2 : 1];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = D2 / 2;
-  const bool tab = D2 <= RWP_MAX_D2;
-  float* cs = cs_l[wave];
-  float* sn = sn_l[wave];
+  const int nch = half >> 3;           // VEC: 8-dim chunks per half
+  const int items = H * nch;           // VEC: (head, chunk) items of a position
+  float* cs = cs_l[TAB ? wave : 0];
+  float* sn = sn_l[TAB ? wave : 0];
   const long npos = (long)S * B;
   for (long pidx = (long)blockIdx.x * RWP_WAVES + wave; pidx < npos; pidx += (long)gridDim.x * RWP_WAVES) {
     const int ss = (int)(pidx / B), bb = (int)(pidx % B);
     const float* f = freqs + ((long)bb * S + ss) * D2;
-    auto cosv = [&](int d) { return tab ? cs[d] : (float)cos((double)f[d]); };
-    auto sinv = [&](int d) { return tab ? sn[d] : (float)sin((double)f[d]); };
-    if (tab) {
-      for (int d = lane; d < D2; d += 64) {
+    auto cosv = [&](int d) {
+      if constexpr (TAB) return cs[d];
+      else return (float)cos((double)f[d]);
+    };
+    auto sinv = [&](int d) {
+      if constexpr (TAB) return sn[d];
+      else return (float)sin((double)f[d]);
+    };
+    const long xb = ss * sx_s + bb * sx_b, ob = ss * so_s + bb * so_b;
+    // angle of the lane's first table entry, then (VEC) the lane's first item,
+    // loaded unconditionally (clamped indices, in bounds) and kept raw, so no
+    // branch or conversion makes the wave wait for them before the table
+    const float th0 = TAB ? f[lane < D2 ? lane : D2 - 1] : 0.0f;
+    Raw8<DT> a0r, p0r;
+    if constexpr (VEC) {
+      const int t0 = lane < items ? lane : items - 1;
+      const int hh = t0 / nch, c = 8 * (t0 - hh * nch);
+      a0r = ld8_raw<DT>(x, xb + hh * sx_h + c);
+      p0r = ld8_raw<DT>(x, xb + hh * sx_h + half + c);
+    }
+    if constexpr (TAB) {
+      // every lane evaluates its first entry (clamped), so the angle load is
+      // not sunk behind the x loads into a branch
+      const float c0 = (float)cos((double)th0), s0 = (float)sin((double)th0);
+      if (lane < D2) {
+        cs[lane] = c0;
+        sn[lane] = s0;
+      }
+      for (int d = lane + 64; d < D2; d += 64) {
         const double th = (double)f[d];
         cs[d] = (float)cos(th);
         sn[d] = (float)sin(th);
@@ -104,14 +166,10 @@ __global__ __launch_bounds__(64 * RWP_WAVES) void rope_with_pos_kernel(
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       __builtin_amdgcn_wave_barrier();
     }
-    const long xb = ss * sx_s + bb * sx_b, ob = ss * so_s + bb * so_b;
     if constexpr (VEC) {
-      const int nch = half >> 3;
-      for (int t = lane; t < H * nch; t += 64) {
+      auto rotate = [&](int t, const float (&a)[8], const float (&pp)[8]) {
         const int hh = t / nch, c = 8 * (t - hh * nch);
-        float a[8], pp[8], o1[8], o2[8];
-        ld8<DT>(x, xb + hh * sx_h + c, a);
-        ld8<DT>(x, xb + hh * sx_h + half + c, pp);
+        float o1[8], o2[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           o1[e] = a[e] * cosv(c + e) + (-pp[e]) * sinv(c + e);
@@ -119,6 +177,19 @@ __global__ __launch_bounds__(64 * RWP_WAVES) void rope_with_pos_kernel(
         }
         st8<DT>(out, ob + hh * so_h + c, o1);
         st8<DT>(out, ob + hh * so_h + half + c, o2);
+      };
+      if (lane < items) {
+        float a0[8], p0[8];
+        cvt8<DT>(a0r, a0);
+        cvt8<DT>(p0r, p0);
+        rotate(lane, a0, p0);
+      }
+      for (int t = lane + 64; t < items; t += 64) {
+        const int hh = t / nch, c = 8 * (t - hh * nch);
+        float a[8], pp[8];
+        ld8<DT>(x, xb + hh * sx_h + c, a);
+        ld8<DT>(x, xb + hh * sx_h + half + c, pp);
+        rotate(t, a, pp);
       }
       const int npass = (D - D2) >> 3;
       for (int t = lane; t < H * npass; t += 64) {
@@ -142,7 +213,7 @@ __global__ __launch_bounds__(64 * RWP_WAVES) void rope_with_pos_kernel(
         st1<DT>(out, ob + hh * so_h + d * so_d, ld1<DT>(x, xb + hh * sx_h + d * sx_d));
       }
     }
-    if (tab) {
+    if constexpr (TAB) {
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // reads done before the next position's writes
       __builtin_amdgcn_wave_barrier();
     }
@@ -164,11 +235,56 @@ __device__ __forceinline__ float sum8_lanes(float v) {
 // VGGT 2-D RoPE.  Eight lanes per (token, part in {q,k}, head) row of 64
 // dims: lane j holds dims 8j..8j+7 (one 16-byte load and store), so a wave
 // moves 8 whole 128-byte rows per instruction.  Each 8-lane group handles NR
-// rows, 32 apart, and issues all NR loads before any arithmetic, to keep more
-// bytes in flight per wave.  Lanes 0-3 hold the y half (dims 0..31), 4-7 the
-// x half; within a half, lanes with (j & 2) == 0 hold dims i < 16 and rotate
-// against lane j ^ 2 (DPP quad_perm).  Dead lanes shadow row 0 and store
-// nothing.
+// rows, 32 apart.  Lanes 0-3 hold the y half (dims 0..31), 4-7 the x half;
+// within a half, lanes with (j & 2) == 0 hold dims i < 16 and rotate against
+// lane j ^ 2 (DPP quad_perm).  Dead lanes shadow row 0 and store nothing.
+// The loads run in three phases, fenced from the compiler's scheduler (which
+// otherwise sinks each load next to its use and so serialises their
+// latencies): every row's token position, then every row's data, then --
+// once the positions are in, with the data still in flight -- every row's
+// cos / sin table entries.
+__device__ __forceinline__ void row_coords(long r, int H, int hshift, int& tok, int& part, int& head) {
+  if (hshift >= 0) {                        // H = 2^hshift: shifts instead of 64-bit divisions
+    tok = (int)(r >> (hshift + 1));
+    part = (int)(r >> hshift) & 1;
+    head = (int)r & ((1 << hshift) - 1);
+  } else {
+    tok = (int)(r / (2 * H));
+    const int rr = (int)(r % (2 * H));
+    part = rr / H;
+    head = rr % H;
+  }
+}
+
+// cos / sin of the 8 frequencies i0 .. i0 + 7 of table row p (clamped to the table)
+struct Angles8 {
+  float4 c0, c1, s0, s1;
+};
+__device__ __forceinline__ Angles8 load_angles(const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                               int p, int P, int i0) {
+  p = p < 0 ? 0 : (p >= P ? P - 1 : p);
+  const float4* cp = reinterpret_cast<const float4*>(cos_t + p * 16 + i0);
+  const float4* sp = reinterpret_cast<const float4*>(sin_t + p * 16 + i0);
+  return Angles8{cp[0], cp[1], sp[0], sp[1]};
+}
+
+// the rotation of one lane's 8 packed fp16 values y against lane j ^ 2's
+__device__ __forceinline__ uint4 rotate8(const uint32_t (&yw)[4], const Angles8& a, bool lo) {
+  const float cs[8] = {a.c0.x, a.c0.y, a.c0.z, a.c0.w, a.c1.x, a.c1.y, a.c1.z, a.c1.w};
+  // the first of a rotation pair subtracts the partner term: x*c - o*s = x*c + o*(-s)
+  const float sg = lo ? -1.0f : 1.0f;
+  const float sn[8] = {sg * a.s0.x, sg * a.s0.y, sg * a.s0.z, sg * a.s0.w,
+                       sg * a.s1.x, sg * a.s1.y, sg * a.s1.z, sg * a.s1.w};
+  uint32_t ow[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)yw[m], 0x4E, 0xF, 0xF, true);  // lane j ^ 2
+    ow[m] = pack2<false>(mix_mul<0>(cs[2 * m], yw[m]) + mix_mul<0>(sn[2 * m], other),
+                         mix_mul<1>(cs[2 * m + 1], yw[m]) + mix_mul<1>(sn[2 * m + 1], other));
+  }
+  return make_uint4(ow[0], ow[1], ow[2], ow[3]);
+}
+
 template <int NR>
 __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                           const int* __restrict__ pos, const float* __restrict__ cos_t,
@@ -177,53 +293,37 @@ __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict_
   const long nrows = (long)T * 2 * H;
   const long g0 = (long)blockIdx.x * (32 * NR) + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
+  const int half = j >> 2;
+  const int i0 = 8 * (j & 1);
+  const bool lo = (j & 2) == 0;
   uint32_t xw[NR][4];   // the row's 8 fp16 values, packed (read through v_fma_mix_f32)
   bool live[NR];
-  int tokv[NR];
-  long doff[NR];
+  int pv[NR];
+  long soff[NR], doff[NR];
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
     const long r = g0 + 32 * k;
     live[k] = r < nrows;
-    const long rc = live[k] ? r : 0;
     int tok, part, head;
-    if (hshift >= 0) {                        // H = 2^hshift: shifts instead of 64-bit divisions
-      tok = (int)(rc >> (hshift + 1));
-      part = (int)(rc >> hshift) & 1;
-      head = (int)rc & ((1 << hshift) - 1);
-    } else {
-      tok = (int)(rc / (2 * H));
-      const int rr = (int)(rc % (2 * H));
-      part = rr / H;
-      head = rr % H;
-    }
-    tokv[k] = tok;
+    row_coords(live[k] ? r : 0, H, hshift, tok, part, head);
+    soff[k] = (long)tok * src_tok + (long)part * H * 64 + (long)head * 64 + 8 * j;
     doff[k] = (long)tok * dst_tok + (long)part * dst_part + (long)head * 64 + 8 * j;
-    const uint4 v = ld_stream16(src + (size_t)tok * src_tok + (size_t)part * H * 64 + (size_t)head * 64 + 8 * j);
-    xw[k][0] = v.x; xw[k][1] = v.y; xw[k][2] = v.z; xw[k][3] = v.w;
+    pv[k] = pos[2 * tok + half];
   }
-  const int half = j >> 2;
-  const int i0 = 8 * (j & 1);
-  const bool lo = (j & 2) == 0;
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
-    int p = pos[2 * tokv[k] + half];
-    p = p < 0 ? 0 : (p >= P ? P - 1 : p);
-    const float4* cp = reinterpret_cast<const float4*>(cos_t + p * 16 + i0);
-    const float4* sp = reinterpret_cast<const float4*>(sin_t + p * 16 + i0);
-    const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
-    const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    // the first of a rotation pair subtracts the partner term: x*c - o*s = x*c + o*(-s)
-    const float sg = lo ? -1.0f : 1.0f;
-    const float sn[8] = {sg * s0.x, sg * s0.y, sg * s0.z, sg * s0.w, sg * s1.x, sg * s1.y, sg * s1.z, sg * s1.w};
-    uint32_t ow[4];
+    const uint4 v = ld_stream16(src + soff[k]);
+    xw[k][0] = v.x; xw[k][1] = v.y; xw[k][2] = v.z; xw[k][3] = v.w;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  Angles8 an[NR];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)xw[k][m], 0x4E, 0xF, 0xF, true);  // lane j ^ 2
-      ow[m] = pack2<false>(mix_mul<0>(cs[2 * m], xw[k][m]) + mix_mul<0>(sn[2 * m], other),
-                           mix_mul<1>(cs[2 * m + 1], xw[k][m]) + mix_mul<1>(sn[2 * m + 1], other));
-    }
-    if (live[k]) st_stream16(dst + doff[k], make_uint4(ow[0], ow[1], ow[2], ow[3]));
+  for (int k = 0; k < NR; ++k) an[k] = load_angles(cos_t, sin_t, pv[k], P, i0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const uint4 o = rotate8(xw[k], an[k], lo);
+    if (live[k]) st_stream16(dst + doff[k], o);
   }
 }
 
@@ -246,42 +346,40 @@ __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
   const long nrows = (long)T * 2 * H;
   const long g0 = (long)blockIdx.x * (QKN_ROWS_PER_WG * NR) + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
+  const int half = j >> 2;
+  const int i0 = 8 * (j & 1);
+  const bool lo = (j & 2) == 0;
   // the row's 8 fp16 values stay packed (pairs 2m, 2m+1 in word m) and enter
   // the fp32 arithmetic through v_fma_mix_f32 (mix_add / mix_mul), which
   // converts exactly for free: the same values as converting first
   uint32_t xw[NR][4];
   bool live[NR];
-  int tokv[NR], partv[NR];
+  int partv[NR], pv[NR];
   uint16_t* row[NR];
+  // load phases as in rope2d_kernel: positions, rows and the q / k norm
+  // weights, then (positions in) the cos / sin entries
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
     const long r = g0 + QKN_ROWS_PER_WG * k;
     live[k] = r < nrows;
-    const long rc = live[k] ? r : 0;          // dead lanes shadow row 0 and store nothing
     int tok, part, head;
-    if (hshift >= 0) {                        // H = 2^hshift: shifts instead of 64-bit divisions
-      tok = (int)(rc >> (hshift + 1));
-      part = (int)(rc >> hshift) & 1;
-      head = (int)rc & ((1 << hshift) - 1);
-    } else {
-      tok = (int)(rc / (2 * H));
-      const int rr = (int)(rc % (2 * H));
-      part = rr / H;
-      head = rr % H;
-    }
-    tokv[k] = tok;
+    row_coords(live[k] ? r : 0, H, hshift, tok, part, head);   // dead lanes shadow row 0
     partv[k] = part;
     row[k] = qkv + (size_t)tok * tok_stride + (size_t)part * H * 64 + (size_t)head * 64;
+    pv[k] = pos[2 * tok + half];
+  }
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
     const uint4 v = ld_stream16(row[k] + 8 * j);
     xw[k][0] = v.x; xw[k][1] = v.y; xw[k][2] = v.z; xw[k][3] = v.w;
   }
-  const int half = j >> 2;
-  const int i0 = 8 * (j & 1);
-  const bool lo = (j & 2) == 0;
-  // q and k norm weights for this lane's 8 dims, fetched with the rows rather
-  // than after the statistics
   const uint4 gq = reinterpret_cast<const uint4*>(qg)[j], bq = reinterpret_cast<const uint4*>(qb)[j];
   const uint4 gk = reinterpret_cast<const uint4*>(kg)[j], bk = reinterpret_cast<const uint4*>(kb)[j];
+  __builtin_amdgcn_sched_barrier(0);
+  Angles8 an[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) an[k] = load_angles(cos_t, sin_t, pv[k], P, i0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
     float s = 0.f;
@@ -308,23 +406,8 @@ __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
     for (int m = 0; m < 4; ++m)
       yw[m] = pack2<false>(mix_add<0>(bw[m], mix_mul<0>(d[2 * m] * rs, gw[m])),
                            mix_add<1>(bw[m], mix_mul<1>(d[2 * m + 1] * rs, gw[m])));
-    int p = pos[2 * tokv[k] + half];
-    p = p < 0 ? 0 : (p >= P ? P - 1 : p);
-    const float4* cp = reinterpret_cast<const float4*>(cos_t + p * 16 + i0);
-    const float4* sp = reinterpret_cast<const float4*>(sin_t + p * 16 + i0);
-    const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
-    const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    // the first of a rotation pair subtracts the partner term: x*c - o*s = x*c + o*(-s)
-    const float sg = lo ? -1.0f : 1.0f;
-    const float sn[8] = {sg * s0.x, sg * s0.y, sg * s0.z, sg * s0.w, sg * s1.x, sg * s1.y, sg * s1.z, sg * s1.w};
-    uint32_t ow[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)yw[m], 0x4E, 0xF, 0xF, true);  // lane j ^ 2
-      ow[m] = pack2<false>(mix_mul<0>(cs[2 * m], yw[m]) + mix_mul<0>(sn[2 * m], other),
-                           mix_mul<1>(cs[2 * m + 1], yw[m]) + mix_mul<1>(sn[2 * m + 1], other));
-    }
-    if (live[k]) st_stream16(row[k] + 8 * j, make_uint4(ow[0], ow[1], ow[2], ow[3]));
+    const uint4 o = rotate8(yw, an[k], lo);
+    if (live[k]) st_stream16(row[k] + 8 * j, o);
   }
 }
 
@@ -376,15 +459,17 @@ extern "C" int qv_rope_with_pos(const void* x, const float* freqs, void* out, in
   const bool vec = xs[3] == 1 && os[3] == 1 && (D2 / 2) % 8 == 0 && (D - D2) % 8 == 0 &&
                    xs[0] % align == 0 && xs[1] % align == 0 && xs[2] % align == 0 && os[0] % align == 0 &&
                    os[1] % align == 0 && os[2] % align == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)out % 16) == 0;
+  const bool tab = D2 <= RWP_MAX_D2;
   const long npos = S * B;
   const long blocks = (npos + RWP_WAVES - 1) / RWP_WAVES;
   const dim3 grid((unsigned)(blocks < 16384 ? blocks : 16384)), block(64 * RWP_WAVES);
   hipStream_t st = (hipStream_t)stream;
-#define QV_ROPE(DTV, V)                                                                                        \
-  hipLaunchKernelGGL((rope_with_pos_kernel<DTV, V>), grid, block, 0, st, x, freqs, out, (int)S, (int)B, (int)H, \
+#define QV_ROPE(DTV, V, T)                                                                                        \
+  hipLaunchKernelGGL((rope_with_pos_kernel<DTV, V, T>), grid, block, 0, st, x, freqs, out, (int)S, (int)B, (int)H, \
                      (int)D, (int)D2, xs[0], xs[1], xs[2], xs[3], os[0], os[1], os[2], os[3])
 #define QV_ROPE_DT(DTV) \
-  if (vec) QV_ROPE(DTV, true); else QV_ROPE(DTV, false);
+  if (vec && tab) QV_ROPE(DTV, true, true); else if (vec) QV_ROPE(DTV, true, false); \
+  else if (tab) QV_ROPE(DTV, false, true); else QV_ROPE(DTV, false, false);
   switch (dtype) {
     case QV_F16: QV_ROPE_DT(QV_F16) break;
     case QV_BF16: QV_ROPE_DT(QV_BF16) break;

@@ -303,15 +303,18 @@ def test_vggt_layer_norm_bit_exact(gpu, M):
 # ------------------------------------------------------------------ RoPE
 @pytest.mark.parametrize("dt", [torch.float16, torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("transpose_out", [False, True])
-@pytest.mark.parametrize("shape", [(37, 3, 16, 64, 48), (5, 2, 3, 40, 20), (3, 1, 2, 1040, 1032), (2, 2, 1, 1040, 1024)],
-                         ids=["vec", "elementwise", "wide_elementwise", "wide_vec"])
+@pytest.mark.parametrize("shape", [(37, 3, 16, 64, 48), (7, 2, 16, 128, 128), (5, 2, 3, 40, 20), (3, 1, 2, 1040, 1032),
+                                   (2, 2, 1, 1040, 1024)],
+                         ids=["vec", "vec_two_items", "elementwise", "wide_elementwise", "wide_vec"])
 def test_fused_rope_with_pos(gpu, transpose_out, dt, shape):
     """fused_rope_with_pos.cu:155-161 dispatches float, half and bfloat16.
     fp16 / bf16 within one ulp of the oracle's rounding (and equal in more
     than 99.9 % of elements), fp32 within 2e-6 relative.  The shapes take the
-    kernel's paths: 16-byte chunks (d2/2 and d - d2 multiples of 8), element
-    accesses (d2/2 = 10; d2/2 = 516), and d2 > 512, where the cos / sin of
-    the angles are evaluated per element instead of once per position."""
+    kernel's paths: 16-byte chunks (d2/2 and d - d2 multiples of 8; fewer
+    (head, chunk) items than lanes with pass-through dims, and two items per
+    lane with a two-pass angle table), element accesses (d2/2 = 10;
+    d2/2 = 516), and d2 > 512, where the cos / sin of the angles are
+    evaluated per element instead of once per position."""
     from qvggt_amd import awq_inference_engine as E
     rng = _rng(3)
     S, B, H, D, D2 = shape
