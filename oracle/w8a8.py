@@ -241,6 +241,9 @@ def gelu_and_quant(x: np.ndarray):
     # act.cu:49-50: `if ((float)t > amax_val) amax_val = (float)t` from 0, so a
     # NaN never enters the maximum (fmax skips it)
     amax = np.fmax.reduce(folded, axis=1, initial=F32(0.0)).astype(F32)
+    # the strict comparison from +0 never takes a -0 (a zero t folds to -0):
+    # a row with no folded value above zero keeps amax = +0
+    amax = np.where(amax > 0, amax, F32(0.0)).astype(F32)
     scale = (amax / F32(127.0)).astype(F32).astype(F16)
     with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
         inv = (F32(127.0) / amax).astype(F32).astype(F16).astype(np.float64)

@@ -203,6 +203,46 @@ def test_gelu_and_quant_bit_exact(gpu, M, D):
     assert torch.equal(q2, q) and torch.equal(s2, s)
 
 
+def test_gelu_and_quant_rows_near_the_fold_floor(gpu):
+    """Rows whose largest |GELU| sits just below, at and just above fp16(1e-4)
+    (the act.cu:47-48 fold floor) and around the smallest maximum for which
+    fp16(127 / amax) is finite, rows whose maximum comes from a negative
+    value, and an all-zero row, bit for bit against the oracle: the kernel
+    takes a shortcut only for rows with a finite maximum above the floor and
+    a finite multiplier."""
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(11)
+    D = 1024
+    rows = []
+    for top in (1.5e-4, 2.0e-4, 2.0003e-4, 2.0004e-4, 2.1e-4, 3e-4, 1e-2):   # GELU(x) ~ x / 2 here
+        rows.append(rng.uniform(0, top, D))
+        rows.append(-rng.uniform(0, top, D))
+        r = rng.uniform(0, top / 4, D)
+        r[rng.integers(D)] = -top
+        rows.append(r)
+    big_neg = rng.uniform(0, 1.5e-4, D)
+    big_neg[::97] = -3.0                   # maximum from GELU(-3) ~ -0.004
+    rows += [big_neg, np.zeros(D)]
+    x = np.stack(rows).astype(np.float16)
+    # x = 0x0A8E, 0x0A8F, 0x0A90 (and negated) give |GELU| = fp16(1e-4) and
+    # the next two fp16 values up; x = 0x1BEA .. 0x1BEC and 0x9BF6 .. 0x9BF8
+    # give |GELU| = 0x17F0 .. 0x17F2 around 0x17F1, the smallest row maximum
+    # whose fp16(127 / amax) is finite: one such element in a row of smaller ones
+    edge = []
+    for b in (0x0A8E, 0x0A8F, 0x0A90, 0x8A8E, 0x8A8F, 0x8A90, 0x1BEA, 0x1BEB, 0x1BEC, 0x9BF6, 0x9BF7, 0x9BF8):
+        r = rng.uniform(-1e-4, 1e-4, D).astype(np.float16)
+        r[rng.integers(D)] = np.uint16(b).view(np.float16)
+        edge.append(r)
+    x = np.concatenate([x, np.stack(edge)])
+    q = torch.empty(x.shape, dtype=torch.int8, device=gpu)
+    s = torch.empty(x.shape[0], dtype=torch.float16, device=gpu)
+    E.gelu_and_quant(q, torch.from_numpy(x).to(gpu), s, None)
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        qr, sr, _ = Q.gelu_and_quant(x)
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+    assert np.array_equal(q.cpu().numpy(), qr)
+
+
 def test_gelu_every_finite_fp16_input(gpu):
     """The fp16 GELU (and its tanh table) on all 63488 finite fp16 values,
     bit for bit against the oracle."""

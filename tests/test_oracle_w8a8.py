@@ -208,15 +208,22 @@ def test_gelu_and_quant_scale_semantics():
 
 def test_gelu_and_quant_amax_skips_nan_like_the_reference_loop():
     """act.cu:44-50 keeps amax with `if ((float)t > amax) amax = t` from 0, so a
-    NaN GELU output (from NaN or -inf input) never enters the maximum."""
-    x = np.random.default_rng(9).standard_normal((3, 64)).astype(np.float16)
+    NaN GELU output (from NaN or -inf input) never enters the maximum, and a
+    row whose values all fold to zero or below (all zeros: the fold gives -0;
+    tiny positives: they fold negative) keeps amax = +0, scale +0."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((6, 64)).astype(np.float16)
     x[0, 5] = np.nan
     x[1, 9] = -np.inf
     x[2, 0] = np.inf
-    with np.errstate(over="ignore", invalid="ignore"):
+    x[3] = 0.0
+    x[4] = rng.uniform(0, 1.5e-4, 64).astype(np.float16)     # GELU in (0, 1e-4]
+    x[5] = -x[4]
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
         q, s, tmp = Q.gelu_and_quant(x)
+    assert s[3].view(np.uint16) == 0 and s[4].view(np.uint16) == 0 and (q[3] == 0).all()
     zero = np.float32(np.float16(0.0001))
-    for r in range(3):
+    for r in range(6):
         amax = np.float32(0.0)
         for t in tmp[r].astype(np.float32):
             f = t if t > zero else -t
