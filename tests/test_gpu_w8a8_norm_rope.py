@@ -285,6 +285,42 @@ def test_per_token_quant_and_ln_quant_with_nan_rows_match_oracle(gpu):
     assert np.array_equal(q.cpu().numpy(), qr)
 
 
+def test_quant_and_ln_quant_row_edge_cases_match_oracle(gpu):
+    """Rows at the edges of the kernels' row-level checks, bit for bit against
+    the oracle: +-inf, a row of fp16 subnormals, a maximum of +-65504, a single
+    non-zero element (per-token quant); LayerNorm outputs so small that amax
+    falls below the smallest normal fp16, and rows with inf (LN + quant)."""
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(12)
+    D = 1024
+    x = (rng.standard_normal((8, D)) * 2).astype(np.float16)
+    x[0, 3] = np.inf
+    x[1, 9] = -np.inf
+    x[2] = (rng.integers(-1023, 1024, D) * 2.0 ** -24).astype(np.float16)   # subnormals
+    x[3, 100] = 65504
+    x[4, 200] = -65504
+    x[5] = 0
+    x[5, 7] = -3.0
+    xd = torch.from_numpy(x).to(gpu)
+    q = torch.empty(x.shape, dtype=torch.int8, device=gpu)
+    s = torch.empty(x.shape[0], dtype=torch.float16, device=gpu)
+    E.invoke_quant(q, xd, s)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        qr, sr = Q.quant_per_token(x)
+    assert np.array_equal(_bits(s), sr.view(np.int16))
+    assert np.array_equal(q.cpu().numpy(), qr)
+    # LN + quant: gamma / beta of 1e-5 .. 1e-3 scale the outputs to around and
+    # below fp16's smallest normal (6.1e-5); rows 0 and 1 hold an inf
+    for gs in (1e-5, 3e-5, 1e-4, 1e-3):
+        g = (gs * (1 + 0.1 * rng.standard_normal(D))).astype(np.float16)
+        b = (0.1 * gs * rng.standard_normal(D)).astype(np.float16)
+        E.rms_norm_general(q, xd, torch.from_numpy(g).to(gpu), torch.from_numpy(b).to(gpu), s, 1e-6, True)
+        with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+            qr, sr = Q.layernorm_quant(x, g, b, 1e-6)
+        assert np.array_equal(_bits(s), sr.view(np.int16)), gs
+        assert np.array_equal(q.cpu().numpy(), qr), gs
+
+
 def test_gelu_non_finite_inputs_match_oracle(gpu):
     """+-inf and NaN in some rows (others finite), bit for bit against the
     oracle: the GELU output, the per-row scale and the int8 values."""
