@@ -3,9 +3,10 @@
 // qv_rope_with_pos: fused_rope_with_pos_forward_func of the reference
 // (rope_new/fused_rope_with_pos.cu:19-164): rotate-half RoPE on the first d2
 // dims of x[s][b][h][:] (arbitrary element strides) with fp32 angles
-// freqs[b][s][0:d2]; dims >= d2 are copied.  cos/sin are evaluated in fp64 and
-// rounded to fp32 (the reference used the fast-math sincosf), once per
-// (s, b, d) and shared by the heads.
+// freqs[b][s][0:d2]; dims >= d2 are copied.  cos/sin are evaluated in fp64
+// (one sincos: a shared argument reduction) and rounded to fp32 (the
+// reference used the fast-math sincosf), once per (s, b, d) and shared by the
+// heads.
 //
 // qv_rope2d: the VGGT 2-D RoPE on the q and k parts of a fused qkv buffer
 // (tokens, 3, H, 64).  Head dims [0,32) rotate with the token's y position,
@@ -152,15 +153,18 @@ __global__ __launch_bounds__(64 * RWP_WAVES) void rope_with_pos_kernel(
     if constexpr (TAB) {
       // every lane evaluates its first entry (clamped), so the angle load is
       // not sunk behind the x loads into a branch
-      const float c0 = (float)cos((double)th0), s0 = (float)sin((double)th0);
+      double sd0, cd0;
+      sincos((double)th0, &sd0, &cd0);
+      const float c0 = (float)cd0, s0 = (float)sd0;
       if (lane < D2) {
         cs[lane] = c0;
         sn[lane] = s0;
       }
       for (int d = lane + 64; d < D2; d += 64) {
-        const double th = (double)f[d];
-        cs[d] = (float)cos(th);
-        sn[d] = (float)sin(th);
+        double sd, cd;
+        sincos((double)f[d], &sd, &cd);
+        cs[d] = (float)cd;
+        sn[d] = (float)sd;
       }
       // the wave's LDS accesses run in order: make the compiler keep them so
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
