@@ -219,6 +219,27 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
+  // the bias values of the wave's columns, all requested before the barrier
+  // (each of the NT x 4 column groups waited for its own load otherwise)
+  uint2 bv[NT][4];
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + 64 * wave + 32 * j + 8 * q + 4 * h;
+      bv[j][q] = epi_has_bias<EPI>() && EPI != QV_EPI_QKROPE ? *reinterpret_cast<const uint2*>(bias + (n < N ? n : 0))
+                                                             : make_uint2(0, 0);
+    }
+  // q/k RoPE: the token positions of the lane's MT rows, likewise early (the
+  // cos / sin reads depend on them)
+  int2 ppv[EPI == QV_EPI_QKROPE ? MT : 1];
+  if constexpr (EPI == QV_EPI_QKROPE) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int m = m0 + 32 * i + l32;
+      ppv[i] = *reinterpret_cast<const int2*>(qk.pos + 2 * (m < M ? m : M - 1));
+    }
+  }
   lds_barrier();
   uint8_t* stg = lds + wave * (BM * EP);
   bool staged = false;
@@ -237,8 +258,6 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
       const uint16_t* bp = is_k ? qk.kb : qk.qb;
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        const int m = m0 + 32 * i + l32;
-        const int mc = m < M ? m : M - 1;
         uint32_t yw[NT][4][2];
         float sum = 0.f;
 #pragma unroll
@@ -273,7 +292,7 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
             }
         pair32(s2, pa, pb);
         const float rs = 1.0f / __builtin_sqrtf((pa + pb) * (1.0f / 64.0f) + qk.eps);
-        const int2 pp = *reinterpret_cast<const int2*>(qk.pos + 2 * mc);
+        const int2 pp = ppv[i];
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
           int p = j == 0 ? pp.x : pp.y;
@@ -325,7 +344,8 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         float r[4] = {acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
-        epilogue_apply4<BF16, EPI>(bias, r, n < N ? n : 0);
+        if constexpr (EPI == QV_EPI_QKROPE) epilogue_apply4<BF16, EPI>(bias, r, n < N ? n : 0);   // v heads
+        else epilogue_apply4v<BF16, EPI>(bv[j][q], r);
         uint2 o;
         o.x = pack2<BF16>(r[0], r[1]);
         o.y = pack2<BF16>(r[2], r[3]);
@@ -336,17 +356,38 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
   __builtin_amdgcn_wave_barrier();
+  // Write-back: iteration it moves row (it * 64 + lane) / 8 of the wave's
+  // tile, 16-byte chunk lane % 8 -- the same 8 columns in every iteration.
+  constexpr int IT = BM * 8 / 64;
+  const int c = lane & 7;
+  const int n = n0 + 64 * wave + 8 * c;
+  if constexpr (EPI == QV_EPI_BIAS_RESID) {
+    // The residual rows are read in place of the output; every read is
+    // issued before the first store (the compiler cannot move a read of
+    // `out` past a store to it, and in the loop below each read waited for
+    // the previous iteration's store: IT serial memory latencies), and
+    // gamma, the same in every iteration, is read once.
+    const uint4 gv = n < N ? *reinterpret_cast<const uint4*>(gamma + n) : make_uint4(0, 0, 0, 0);
+    uint4 rv[IT];
 #pragma unroll
-  for (int it = 0; it < BM * 8 / 64; ++it) {
-    const int idx = it * 64 + lane;
-    const int row = idx >> 3, c = idx & 7;
-    const int m = m0 + row, n = n0 + 64 * wave + 8 * c;
-    if (m < M && n < N) {
-      uint4 v = *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16));
-      if constexpr (EPI == QV_EPI_BIAS_RESID)
-        v = resid_update8<BF16>(*reinterpret_cast<const uint4*>(out + (size_t)m * N + n), v,
-                                *reinterpret_cast<const uint4*>(gamma + n));
-      st_stream16(out + (size_t)m * N + n, v);
+    for (int it = 0; it < IT; ++it) {
+      const int m = m0 + ((it * 64 + lane) >> 3);
+      rv[it] = m < M && n < N ? *reinterpret_cast<const uint4*>(out + (size_t)m * N + n) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int row = (it * 64 + lane) >> 3;
+      const int m = m0 + row;
+      if (m < M && n < N)
+        st_stream16(out + (size_t)m * N + n,
+                    resid_update8<BF16>(rv[it], *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16)), gv));
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int row = (it * 64 + lane) >> 3;
+      const int m = m0 + row;
+      if (m < M && n < N) st_stream16(out + (size_t)m * N + n, *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16)));
     }
   }
 }

@@ -262,17 +262,36 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
     __builtin_amdgcn_wave_barrier();
     uint16_t* o16 = reinterpret_cast<uint16_t*>(out);
+    // Write-back: iteration it moves row (it * 64 + lane) / 8 of the wave's
+    // tile, 16-byte chunk lane % 8 -- the same 8 columns in every iteration.
+    constexpr int IT = BM * 8 / 64;
+    const int c = lane & 7;
+    const int n = n0 + 64 * wave + 8 * c;
+    if constexpr (OUT == 3) {
+      // residual rows read in place of the output, all before the first
+      // store (a read of `out` cannot move past a store to it, so in one loop
+      // each read waited for the previous store); gamma read once
+      const uint4 gv = n < N ? *reinterpret_cast<const uint4*>(gamma + n) : make_uint4(0, 0, 0, 0);
+      uint4 rv[IT];
 #pragma unroll
-    for (int it = 0; it < BM * 8 / 64; ++it) {
-      const int idx = it * 64 + lane;
-      const int row = idx >> 3, c = idx & 7;
-      const int m = m0 + row, n = n0 + 64 * wave + 8 * c;
-      if (m < M && n < N) {
-        uint4 v = *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16));
-        if constexpr (OUT == 3)
-          v = resid_update8<false>(*reinterpret_cast<const uint4*>(o16 + (size_t)m * N + n), v,
-                                   *reinterpret_cast<const uint4*>(gamma + n));
-        st_stream16(o16 + (size_t)m * N + n, v);
+      for (int it = 0; it < IT; ++it) {
+        const int m = m0 + ((it * 64 + lane) >> 3);
+        rv[it] = m < M && n < N ? *reinterpret_cast<const uint4*>(o16 + (size_t)m * N + n) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int row = (it * 64 + lane) >> 3;
+        const int m = m0 + row;
+        if (m < M && n < N)
+          st_stream16(o16 + (size_t)m * N + n,
+                      resid_update8<false>(rv[it], *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16)), gv));
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int row = (it * 64 + lane) >> 3;
+        const int m = m0 + row;
+        if (m < M && n < N) st_stream16(o16 + (size_t)m * N + n, *reinterpret_cast<const uint4*>(stg + stg_off(row, c * 16)));
       }
     }
   }
