@@ -122,32 +122,18 @@ struct QkRopeArgs {
   float eps = 0.f;
 };
 
-// Bias / GELU on four consecutive channels n..n+3 (fp32, before the single
-// rounding to the 16-bit output type).
+// whether an epilogue adds a bias
 template <int EPI>
 constexpr bool epi_has_bias() {
   return EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_BIAS_RESID || EPI == QV_EPI_QKROPE;
 }
 
-// The same with the four bias values already loaded (b; ignored without bias).
+// Bias / GELU on four consecutive channels (fp32, before the single rounding
+// to the 16-bit output type); b holds their four bias values, already loaded
+// (ignored without bias).
 template <bool BF16, int EPI>
 __device__ __forceinline__ void epilogue_apply4v(const uint2& b, float (&r)[4]) {
   if constexpr (epi_has_bias<EPI>()) {
-    r[0] += to_f32((uint16_t)(b.x & 0xFFFF), BF16);
-    r[1] += to_f32((uint16_t)(b.x >> 16), BF16);
-    r[2] += to_f32((uint16_t)(b.y & 0xFFFF), BF16);
-    r[3] += to_f32((uint16_t)(b.y >> 16), BF16);
-  }
-  if constexpr (EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_GELU) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = gelu_erf(r[i]);
-  }
-}
-
-template <bool BF16, int EPI>
-__device__ __forceinline__ void epilogue_apply4(const uint16_t* __restrict__ bias, float (&r)[4], int n) {
-  if constexpr (epi_has_bias<EPI>()) {
-    const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
     r[0] += to_f32((uint16_t)(b.x & 0xFFFF), BF16);
     r[1] += to_f32((uint16_t)(b.x >> 16), BF16);
     r[2] += to_f32((uint16_t)(b.y & 0xFFFF), BF16);

@@ -227,8 +227,7 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int n = n0 + 64 * wave + 32 * j + 8 * q + 4 * h;
-      bv[j][q] = epi_has_bias<EPI>() && EPI != QV_EPI_QKROPE ? *reinterpret_cast<const uint2*>(bias + (n < N ? n : 0))
-                                                             : make_uint2(0, 0);
+      bv[j][q] = epi_has_bias<EPI>() ? *reinterpret_cast<const uint2*>(bias + (n < N ? n : 0)) : make_uint2(0, 0);
     }
   // q/k RoPE: the token positions of the lane's MT rows, likewise early (the
   // cos / sin reads depend on them)
@@ -256,6 +255,17 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
       const bool is_k = nw >= (qk.qk_cols >> 1);
       const uint16_t* gp = is_k ? qk.kg : qk.qg;
       const uint16_t* bp = is_k ? qk.kb : qk.qb;
+      // the head's norm weights for the lane's 32 columns, read once for all
+      // MT row blocks (the main loop's registers are free by now)
+      uint2 gv[NT][4], bev[NT][4];
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int dl = 32 * j + 8 * q + 4 * h;
+          gv[j][q] = *reinterpret_cast<const uint2*>(gp + dl);
+          bev[j][q] = *reinterpret_cast<const uint2*>(bp + dl);
+        }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         uint32_t yw[NT][4][2];
@@ -264,10 +274,9 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
         for (int j = 0; j < NT; ++j)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int dl = 32 * j + 8 * q + 4 * h;
-            const uint2 bv = *reinterpret_cast<const uint2*>(bias + nw + dl);
-            yw[j][q][0] = pack2<false>(mix_add<0>(bv.x, acc[j][i][4 * q]), mix_add<1>(bv.x, acc[j][i][4 * q + 1]));
-            yw[j][q][1] = pack2<false>(mix_add<0>(bv.y, acc[j][i][4 * q + 2]), mix_add<1>(bv.y, acc[j][i][4 * q + 3]));
+            const uint2 b2 = bv[j][q];
+            yw[j][q][0] = pack2<false>(mix_add<0>(b2.x, acc[j][i][4 * q]), mix_add<1>(b2.x, acc[j][i][4 * q + 1]));
+            yw[j][q][1] = pack2<false>(mix_add<0>(b2.y, acc[j][i][4 * q + 2]), mix_add<1>(b2.y, acc[j][i][4 * q + 3]));
 #pragma unroll
             for (int w = 0; w < 2; ++w) {
               sum = mix_add<0>(yw[j][q][w], sum);
@@ -300,10 +309,7 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
           uint32_t zw[4][2];   // LayerNorm output of this half, rounded to fp16
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int dl = 32 * j + 8 * q + 4 * h;
-            const uint2 g = *reinterpret_cast<const uint2*>(gp + dl);
-            const uint2 b = *reinterpret_cast<const uint2*>(bp + dl);
-            const uint32_t gw[2] = {g.x, g.y}, bw[2] = {b.x, b.y};
+            const uint32_t gw[2] = {gv[j][q].x, gv[j][q].y}, bw[2] = {bev[j][q].x, bev[j][q].y};
 #pragma unroll
             for (int w = 0; w < 2; ++w)
               zw[q][w] = pack2<false>(mix_add<0>(bw[w], mix_mul<0>(d[j][q][2 * w] * rs, gw[w])),
@@ -340,12 +346,10 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int nl = 32 * j + 8 * q + 4 * h;
-      const int n = n0 + 64 * wave + nl;
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         float r[4] = {acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
-        if constexpr (EPI == QV_EPI_QKROPE) epilogue_apply4<BF16, EPI>(bias, r, n < N ? n : 0);   // v heads
-        else epilogue_apply4v<BF16, EPI>(bv[j][q], r);
+        epilogue_apply4v<BF16, EPI>(bv[j][q], r);
         uint2 o;
         o.x = pack2<BF16>(r[0], r[1]);
         o.y = pack2<BF16>(r[2], r[3]);
