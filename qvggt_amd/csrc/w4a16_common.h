@@ -145,35 +145,6 @@ __device__ __forceinline__ void epilogue_apply4v(const uint2& b, float (&r)[4]) 
   }
 }
 
-// Bias / GELU epilogue on four consecutive channels n..n+3 of token m, one
-// rounding to the 16-bit output type, one 8-byte store.
-template <bool BF16, int EPI>
-__device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, const uint16_t* __restrict__ bias,
-                                                float r0, float r1, float r2, float r3, int m, int n, int N) {
-  float r[4] = {r0, r1, r2, r3};
-  if constexpr (EPI == QV_EPI_BIAS || EPI == QV_EPI_BIAS_GELU) {
-    const uint2 b = *reinterpret_cast<const uint2*>(bias + n);
-    r[0] += to_f32((uint16_t)(b.x & 0xFFFF), BF16);
-    r[1] += to_f32((uint16_t)(b.x >> 16), BF16);
-    r[2] += to_f32((uint16_t)(b.y & 0xFFFF), BF16);
-    r[3] += to_f32((uint16_t)(b.y >> 16), BF16);
-  }
-  if constexpr (EPI == QV_EPI_BIAS_GELU || EPI == QV_EPI_GELU) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = gelu_erf(r[i]);
-  }
-  uint2 o;
-  o.x = pack2<BF16>(r[0], r[1]);
-  o.y = pack2<BF16>(r[2], r[3]);
-  *reinterpret_cast<uint2*>(out + (size_t)m * N + n) = o;
-}
-
-template <bool BF16, int EPI>
-__device__ __forceinline__ void epilogue_store4(uint16_t* __restrict__ out, const uint16_t* __restrict__ bias,
-                                                f32x4 v, int m, int n, int N) {
-  epilogue_store4<BF16, EPI>(out, bias, v[0], v[1], v[2], v[3], m, n, N);
-}
-
 // Tile plan of one streamed launch: rows [0, rows_a) in (32 mt_a)-row tiles
 // and rows [rows_a, M) in (32 mt_b)-row tiles; mt_b = 0: every row in
 // (32 mt_a)-row tiles.  Pairs (4, 3), (4, 2), (3, 2); rows_a a multiple of
