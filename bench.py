@@ -375,6 +375,10 @@ def kernel_suite(dev):
     o = torch.empty(10992, 4096, **f16)
     us = _time_graph(lambda i: E.w8a8_gemm_forward_cuda(a, w, ws_, as_, o), 10)
     r["w8a8_fc1_M10992"] = {"us": round(us, 1), "TOPS": round(2.0 * 10992 * 4096 * 1024 / us / 1e6, 1)}
+    # the same GEMM on the packed weight layout (what the W8A8 linear module runs)
+    wp = E.w8a8_pack_weight(w)
+    us = _time_graph(lambda i: E.w8a8_gemm_packed(a, wp, 4096, ws_, as_, o), 10)
+    r["w8a8_fc1_packed_M10992"] = {"us": round(us, 1), "TOPS": round(2.0 * 10992 * 4096 * 1024 / us / 1e6, 1)}
     # W8A8 MLP pair (W8A8 variant): fc1 + bias, GELU + per-token
     # quant of the hidden activations, fc2 + bias
     x8 = torch.randint(-128, 128, (10992, 1024), dtype=torch.int8, device=dev)
@@ -393,6 +397,16 @@ def kernel_suite(dev):
 
     us = _time_graph(w8_pair, 5)
     r["w8a8_mlp_pair_M10992"] = {"us": round(us, 1), "TOPS": round(2 * 2.0 * 10992 * 4096 * 1024 / us / 1e6, 1)}
+    w2p = E.w8a8_pack_weight(w2)
+
+    def w8_pair_packed(i):
+        E.w8a8_gemm_packed(x8, wp, 4096, ws_, s8, o, bias=b1)
+        E.gelu_and_quant(hq, o, hs, None)
+        E.w8a8_gemm_packed(hq, w2p, 1024, ws2, hs, y8, bias=b2)
+
+    us = _time_graph(w8_pair_packed, 5)
+    r["w8a8_mlp_pair_packed_M10992"] = {"us": round(us, 1),
+                                        "TOPS": round(2 * 2.0 * 10992 * 4096 * 1024 / us / 1e6, 1)}
     return r
 
 

@@ -187,6 +187,25 @@ int qv_w8a8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* out, int64_t M, 
                      int64_t K, void* stream);
 
 /*
+ * Packed W8A8 weights.  No counterpart in the reference: its int8 GEMM reads
+ * the (N, K) weight as stored.  For callers that keep a weight across calls
+ * (the W8A8 linear module), a one-time re-layout lets the GEMM load each
+ * wave's weight fragments straight to registers with one contiguous 1 KB
+ * load per instruction.  qv_w8a8_packed_bytes(N, K) is the packed size
+ * (N rounded up to 32, times K); qv_w8a8_pack_weight writes it from the
+ * (N, K) int8 weight (K a multiple of 64, N of 16).  qv_w8a8_gemm_packed
+ * computes what qv_w8a8_gemm computes (gamma NULL; bias optional), or what
+ * qv_w8a8_gemm_residual computes (gamma given; bias required, `out` the
+ * residual, updated in place), from the packed weight: the same int32
+ * accumulators and fp16 results, bit for bit.
+ */
+int64_t qv_w8a8_packed_bytes(int64_t N, int64_t K);
+int qv_w8a8_pack_weight(const int8_t* w, int8_t* packed, int64_t N, int64_t K, void* stream);
+int qv_w8a8_gemm_packed(const int8_t* a, const int8_t* packed_b, const void* wscales,
+                        const void* ascales, const void* bias, const void* gamma, void* out,
+                        int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
  * Per-token int8 quantisation of x (M,D) (dtype QV_F16/QV_BF16/QV_F32):
  * scale[m] fp16 = amax/127, q = sat(rint(x * 127/amax)).
  * Replaces invoke_quant (w8a8/quantization.h:2-4, quantization.cu:42-96).

@@ -40,6 +40,9 @@ SIGNATURES: dict[str, list] = {
     "qv_w8a8_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "qv_w8a8_gemm_residual": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "qv_w8a8_gemm_i32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "qv_w8a8_packed_bytes": [_i64, _i64],
+    "qv_w8a8_pack_weight": [_vp, _vp, _i64, _i64, _vp],
+    "qv_w8a8_gemm_packed": [_vp] * 7 + [_i64] * 3 + [_vp],
     "qv_quant_per_token": [_vp, _i32, _vp, _vp, _i64, _i64, _vp],
     "qv_layernorm_quant": [_vp, _i32, _vp, _vp, _vp, _vp, _f32, _i32, _i64, _i64, _vp],
     "qv_gelu_quant": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
@@ -50,7 +53,7 @@ SIGNATURES: dict[str, list] = {
     "qv_qknorm_rope2d": [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _f32, _i64, _i64, _i64, _vp],
     "qv_attention_fwd": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _vp],
 }
-_RESTYPES = {"qv_last_error": C.c_char_p, "qv_version": C.c_char_p}
+_RESTYPES = {"qv_last_error": C.c_char_p, "qv_version": C.c_char_p, "qv_w8a8_packed_bytes": C.c_int64}
 
 _lock = threading.Lock()
 _lib = None

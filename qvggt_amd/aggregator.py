@@ -167,10 +167,13 @@ def vggt_positions(S: int, device=None) -> torch.Tensor:
 class W8A8Linear(nn.Module):
     """int8 per-output-channel weights; input is (int8 codes, per-token fp16 scales).
 
-    forward(q, s) = fp16(float(q . W^T) * wscale[n] * s[m] + bias[n]) via the
-    w8a8_gemm_fuse_bias_forward_cuda op.  (No such module exists in the
-    reference; it pairs the W8A8 ops of csrc/w8a8 the way their signatures
-    imply, pybind.cpp:29-36.)
+    forward(q, s) = fp16(float(q . W^T) * wscale[n] * s[m] + bias[n]), what the
+    w8a8_gemm_fuse_bias_forward_cuda op computes.  (No such module exists in
+    the reference; it pairs the W8A8 ops of csrc/w8a8 the way their signatures
+    imply, pybind.cpp:29-36.)  The GEMM runs on a packed copy of ``weight``
+    (``w8a8_pack_weight``), made on first use and again whenever ``weight``
+    is replaced or written in place; results are bit for bit those of the
+    op on ``weight``.
     """
 
     def __init__(self, in_features, out_features, bias=True, dev=None):
@@ -179,6 +182,15 @@ class W8A8Linear(nn.Module):
         self.register_buffer("weight", torch.zeros(out_features, in_features, dtype=torch.int8, device=dev))
         self.register_buffer("wscales", torch.zeros(out_features, dtype=torch.float16, device=dev))
         self.register_buffer("bias", torch.zeros(out_features, dtype=torch.float16, device=dev) if bias else None)
+        self._packed, self._packed_key = None, None
+
+    def packed_weight(self) -> torch.Tensor:
+        """The packed copy of ``weight``, re-made when ``weight`` changed."""
+        w = self.weight
+        key = (w.data_ptr(), w._version, w.device)
+        if self._packed_key != key:
+            self._packed, self._packed_key = E.w8a8_pack_weight(w), key
+        return self._packed
 
     @classmethod
     def from_linear(cls, linear: nn.Linear):
@@ -194,10 +206,7 @@ class W8A8Linear(nn.Module):
     def forward(self, q: torch.Tensor, s: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         M = q.shape[0]
         out = torch.empty(M, self.out_features, dtype=torch.float16, device=q.device) if out is None else out
-        if self.bias is not None:
-            E.w8a8_gemm_fuse_bias_forward_cuda(q, self.weight, self.wscales, s, out, self.bias)
-        else:
-            E.w8a8_gemm_forward_cuda(q, self.weight, self.wscales, s, out)
+        E.w8a8_gemm_packed(q, self.packed_weight(), self.out_features, self.wscales, s, out, bias=self.bias)
         return out
 
     def forward_residual(self, q: torch.Tensor, s: torch.Tensor, gamma: torch.Tensor,
@@ -206,7 +215,9 @@ class W8A8Linear(nn.Module):
         store loop when the layer has a bias, else the GEMM then torch's
         addcmul (the same single rounding of resid + gamma * o)."""
         if self.bias is not None:
-            return E.w8a8_linear_residual(q, self.weight, self.wscales, s, self.bias, gamma, resid)
+            E.w8a8_gemm_packed(q, self.packed_weight(), self.out_features, self.wscales, s, resid,
+                               bias=self.bias, gamma=gamma)
+            return resid
         return resid.addcmul_(self.forward(q, s), gamma)
 
 

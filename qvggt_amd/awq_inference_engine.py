@@ -394,17 +394,23 @@ def _need(t: torch.Tensor, dtype, what: str, name: str):
         _fail(f"{what}: {name} must be contiguous (it is written in place)")
 
 
-def _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, what, gamma=None):
+def _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, what, gamma=None, packed_n=None):
     for name, t, dt in (("in_feats", in_feats, torch.int8), ("kernel", kernel, torch.int8),
                         ("wscales", wscales, torch.float16), ("ascales", ascales, torch.float16),
                         ("out_feats", out_feats, torch.float16)):
         _need(t, dt, what, name)
-    if in_feats.dim() != 2 or kernel.dim() != 2:
+    if in_feats.dim() != 2 or (packed_n is None and kernel.dim() != 2):
         _fail(f"{what}: in_feats and kernel must be 2-D (M,K) and (N,K)")
     M, K = in_feats.shape
-    N = kernel.shape[0]
-    if kernel.shape[1] != K:
-        _fail(f"{what}: K mismatch {K} vs {kernel.shape[1]}")
+    if packed_n is None:
+        N = kernel.shape[0]
+        if kernel.shape[1] != K:
+            _fail(f"{what}: K mismatch {K} vs {kernel.shape[1]}")
+    else:
+        N = int(packed_n)
+        if kernel.dim() != 1 or kernel.numel() != w8a8_packed_bytes(N, K):
+            _fail(f"{what}: packed weight must be 1-D with {w8a8_packed_bytes(N, K)} bytes for N={N} K={K}, "
+                  f"got shape {tuple(kernel.shape)}")
     if out_feats.shape[-2:] != (M, N):
         _fail(f"{what}: out_feats must be (M, N) = ({M}, {N}), got {tuple(out_feats.shape)}")
     if wscales.numel() != N or ascales.numel() != M:
@@ -421,7 +427,10 @@ def _w8a8(in_feats, kernel, wscales, ascales, out_feats, bias, what, gamma=None)
             _fail(f"{what}: the residual form needs the bias")
     dev = _on_gpu(in_feats, kernel, wscales, ascales, out_feats, bias, gamma, what=what)
     with _device(dev):
-        if gamma is None:
+        if packed_n is not None:
+            _lib.call("qv_w8a8_gemm_packed", _ptr(in_feats), _ptr(kernel), _ptr(wscales), _ptr(ascales),
+                      _ptr(bias), _ptr(gamma), _ptr(out_feats), M, N, K, _stream(dev))
+        elif gamma is None:
             _lib.call("qv_w8a8_gemm", _ptr(in_feats), _ptr(kernel), _ptr(wscales), _ptr(ascales), _ptr(bias),
                       _ptr(out_feats), M, N, K, _stream(dev))
         else:
@@ -449,6 +458,40 @@ def w8a8_linear_residual(in_feats, kernel, wscales, ascales, bias, gamma, residu
         _fail(f"{what}: residual must be contiguous")
     _w8a8(in_feats, kernel, wscales, ascales, residual, bias, what, gamma=gamma)
     return residual
+
+
+def w8a8_packed_bytes(N: int, K: int) -> int:
+    """Size in bytes of an (N, K) int8 weight in the packed layout (N rounded up to 32)."""
+    return (N + 31) // 32 * 32 * K
+
+
+def w8a8_pack_weight(kernel: torch.Tensor) -> torch.Tensor:
+    """One-time re-layout of an (N, K) int8 weight for ``w8a8_gemm_packed``: a
+    1-D int8 tensor of ``w8a8_packed_bytes(N, K)`` bytes.  No reference
+    counterpart (the reference's GEMM reads the (N, K) weight as stored); the
+    packed GEMM loads each wave's weight fragments with one contiguous 1 KB
+    load per instruction instead of staging them through LDS."""
+    what = "w8a8_pack_weight"
+    _need(kernel, torch.int8, what, "kernel")
+    if kernel.dim() != 2:
+        _fail(f"{what}: kernel must be 2-D (N, K)")
+    N, K = kernel.shape
+    dev = _on_gpu(kernel, what=what)
+    packed = torch.empty(w8a8_packed_bytes(N, K), dtype=torch.int8, device=dev)
+    with _device(dev):
+        _lib.call("qv_w8a8_pack_weight", _ptr(kernel), _ptr(packed), N, K, _stream(dev))
+    return packed
+
+
+def w8a8_gemm_packed(in_feats, packed, N: int, wscales, ascales, out_feats, bias=None, gamma=None) -> None:
+    """``w8a8_gemm_forward_cuda`` / ``w8a8_gemm_fuse_bias_forward_cuda`` (gamma None)
+    or ``w8a8_linear_residual`` (gamma given, bias required, ``out_feats`` the
+    residual, updated in place) from a ``w8a8_pack_weight`` weight of N output
+    channels: the same results bit for bit."""
+    what = "w8a8_gemm_packed"
+    if gamma is not None and not out_feats.is_contiguous():
+        _fail(f"{what}: residual must be contiguous")
+    _w8a8(in_feats, packed, wscales, ascales, out_feats, bias, what, gamma=gamma, packed_n=N)
 
 
 def w8a8_gemm_int32(in_feats: torch.Tensor, kernel: torch.Tensor) -> torch.Tensor:

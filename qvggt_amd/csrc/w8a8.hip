@@ -15,6 +15,15 @@
 // K-slots: k-step s (0..1) of a stage, lane half h: k = 32*s + 16*h + 0..15
 // (16 contiguous bytes = chunk 2s + h) on both operands.  Output: lane (h, l),
 // register r holds out[m = l][n = 8*(r/4) + 4*h + r%4] of the wave's tile.
+// Packed weights (PACKED, qv_w8a8_gemm_packed): the weights are re-laid out
+// once (qv_w8a8_pack_weight) so that the 16-byte B fragment of lane L for
+// column block cb (32 channels), stage ks and k-step s sits at byte
+// ((cb * KS + ks) * 2 + s) * 1024 + 16 * L: each wave then loads its own
+// 64 columns straight to registers, one stage ahead, every load instruction
+// one contiguous 1 KB, and the LDS holds only the activations.  (Loaded
+// straight from the N x K layout, each 16-byte lane load touches 32 rows in
+// 32-byte pieces: measured 10-26 % slower than the LDS path; packed, 12-16 %
+// faster than it.)
 // Outputs are written with non-temporal stores so that they do not evict the
 // operand rows the XCD's other tiles still read from L2.  The residual form
 // (OUT 3, qv_w8a8_gemm_residual) reads the residual row chunk and LayerScale
@@ -30,7 +39,7 @@ __device__ __forceinline__ int f8(int r) { return (r + (r >> 2)) & 3; }
 
 // OUT: 0 = fp16 (scaled), 1 = fp16 (scaled + bias), 2 = raw int32,
 // 3 = fp16 (scaled + bias) LayerScale-added to `out` in place
-template <int MT, int OUT>
+template <int MT, int OUT, bool PACKED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b,
                       const uint16_t* __restrict__ ws, const uint16_t* __restrict__ as,
@@ -38,12 +47,14 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
                       void* __restrict__ out, int M, int N, int K, int tiles_n, int gn) {
   constexpr bool BIAS = OUT == 1 || OUT == 3;
   constexpr int BM = 32 * MT, BN = 256, NT = 2;
-  constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64;
+  constexpr int A_BYTES = BM * 64, B_BYTES = PACKED ? 0 : BN * 64;
   constexpr int STAGE = A_BYTES + B_BYTES;
   constexpr int NSTAGE = 3;
   constexpr int A_INSTR = BM / 64;   // 1 KB direct loads per wave per stage (A)
-  constexpr int B_INSTR = 4;         // 16 KB / 1 KB / 4 waves
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * STAGE];
+  constexpr int B_INSTR = 4;         // 16 KB / 1 KB / 4 waves (LDS path)
+  constexpr int EP = 128;            // bytes per staged epilogue row (64 fp16, chunk-swizzled: stg_off)
+  constexpr int LDS_BYTES = NSTAGE * STAGE > 4 * BM * EP ? NSTAGE * STAGE : 4 * BM * EP;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -90,7 +101,9 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
   }
 
   const auto rsA = make_rsrc(a + (size_t)m0 * K, (uint64_t)(M - m0) * K);
-  const auto rsB = make_rsrc(b + (size_t)n0 * K, (uint64_t)(N - n0) * K);
+  // packed: column blocks of 32 channels, 32 K bytes each, N rounded up to 32
+  const auto rsB = PACKED ? make_rsrc(b + (size_t)n0 * K, (uint64_t)(((N + 31) & ~31) - n0) * K)
+                          : make_rsrc(b + (size_t)n0 * K, (uint64_t)(N - n0) * K);
 
   // Direct loads: instruction covers 16 rows r0..r0+15 (r0 % 16 == 0); lane L
   // lands at row r0 + L/4, physical chunk L%4, so it fetches logical chunk
@@ -109,10 +122,12 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
       const int r0 = 16 * (A_INSTR * wave + q);
       lds_dma16(rsA, voff[(r0 >> 4) & 1], r0 * K + ks * 64, base + r0 * 64);
     }
+    if constexpr (!PACKED) {
 #pragma unroll
-    for (int q = 0; q < B_INSTR; ++q) {
-      const int r0 = 16 * (B_INSTR * wave + q);
-      lds_dma16(rsB, voff[(r0 >> 4) & 1], r0 * K + ks * 64, base + A_BYTES + r0 * 64);
+      for (int q = 0; q < B_INSTR; ++q) {
+        const int r0 = 16 * (B_INSTR * wave + q);
+        lds_dma16(rsB, voff[(r0 >> 4) & 1], r0 * K + ks * 64, base + A_BYTES + r0 * 64);
+      }
     }
   };
 
@@ -125,62 +140,138 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0;
 
   const int fl = f8(l32);  // f has period 16: f(32*i + l32) == f(l32), and f(64*w + 32*j + l32) too
-  // Fragments of k-step s of the stage in LDS buffer st (weights, activations).
-  auto read = [&](int st, int s, uint4 (&bw)[NT], uint4 (&av)[MT]) {
-    const uint8_t* base = lds + st * STAGE;
-    const uint32_t col = (uint32_t)(((2 * s + h) ^ fl) * 16);
+  if constexpr (PACKED) {
+    // Activation fragments of k-step s of the stage in LDS buffer st.
+    auto read_a = [&](int st, int s, uint4 (&av)[MT]) {
+      const uint8_t* base = lds + st * STAGE;
+      const uint32_t col = (uint32_t)(((2 * s + h) ^ fl) * 16);
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
-      bw[j] = *reinterpret_cast<const uint4*>(base + A_BYTES + (64 * wave + 32 * j + l32) * 64 + col);
+      for (int i = 0; i < MT; ++i) av[i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 64 + col);
+    };
+    // Weights of column block 2 * wave + j, stage ks, k-step s: one 1 KB load.
+    uint32_t b_voff[NT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) av[i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 64 + col);
-  };
-  auto mfmas = [&](const uint4 (&bw)[NT], const uint4 (&av)[MT]) {
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int j = 0; j < NT; ++j) b_voff[j] = (uint32_t)((2 * wave + j) * 32 * K + 16 * lane);
+    auto load_b = [&](int ks, uint4 (&bw)[NT][2]) {
 #pragma unroll
       for (int j = 0; j < NT; ++j)
-        acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bw[j]),
-                                                          __builtin_bit_cast(i32x4, av[i]), acc[j][i], 0, 0, 0);
-  };
-  // One stage (buffer st).  On entry b0 / a0 hold its k-step 0 fragments.
-  // Step 0 issues the reads of step 1, then its MFMAs; step 1 issues the
-  // reads of the NEXT stage's k-step 0 (buffer nst), then its MFMAs, so no
-  // stage starts with its MFMAs waiting behind the barrier for LDS reads.
-  // The fences keep the compiler from sinking each read next to its use.
-  uint4 b0[NT], a0[MT];
-  auto compute = [&](int st, int nst) {
-    uint4 b1[NT], a1[MT];
-    read(st, 1, b1, a1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(b0, a0);
-    __builtin_amdgcn_sched_barrier(0);
-    read(nst, 0, b0, a0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(b1, a1);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // Stage ks uses buffer ks % 3.  At its top: vmcnt(0) lands this wave's
-  // copies of stage ks + 1 (issued one stage earlier), and the barrier makes
-  // every wave's visible and guarantees every wave is done with buffer
-  // (ks + 2) % 3 = the previous stage's, which then receives stage ks + 2.
-  // Stages past KS - 1 are not copied; the last stage's read of the "next"
-  // stage reads a buffer nobody uses again (its values are dropped).
-  issue(0, 0);
-  if (KS > 1) issue(1, 1);
-  // vmcnt(0): stages 0 and 1; lgkmcnt(0), as a builtin the compiler sees:
-  // a scalar load it hoisted here (a kernel argument of the epilogue) would
-  // otherwise count as pending through the loop, and since scalar loads
-  // return out of order the compiler would wait lgkmcnt(0) for every LDS read
-  __builtin_amdgcn_s_waitcnt(0x0070);
-  lds_barrier();
-  read(0, 0, b0, a0);
-  for (int ks = 0; ks < KS; ++ks) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+          bw[j][s2] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsB, b_voff[j], ks * 2048 + 1024 * s2, 0));
+    };
+    auto mfmas = [&](const uint4 (&bw)[NT][2], int s, const uint4 (&av)[MT]) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bw[j][s]),
+                                                            __builtin_bit_cast(i32x4, av[i]), acc[j][i], 0, 0, 0);
+    };
+    // One stage (LDS buffer st, weights bw), as in the LDS path below: step 0
+    // issues the activation reads of step 1, then its MFMAs; step 1 those of
+    // the next stage's step 0 (buffer nst), then its MFMAs.
+    uint4 a0[MT];
+    auto compute = [&](int st, int nst, const uint4 (&bw)[NT][2]) {
+      uint4 a1[MT];
+      read_a(st, 1, a1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(bw, 0, a0);
+      __builtin_amdgcn_sched_barrier(0);
+      read_a(nst, 0, a0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(bw, 1, a1);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // Stage ks uses LDS buffer ks % 3 and weight register set ks & 1.  At its
+    // top: vmcnt(0) lands this wave's activation copy of stage ks + 1 (issued
+    // one stage earlier) and its weights of stage ks; the barrier publishes the
+    // copies and frees buffer (ks + 2) % 3 for stage ks + 2; the weights of stage
+    // ks + 1 go into the idle register set.  Every iteration runs two stages (a
+    // conditional second half made the compiler spill the accumulators); with
+    // an odd stage count the last one multiplies zero weights, which adds
+    // exactly nothing (int8 x 0) whatever stale activations its buffer holds.
+    uint4 bX[NT][2], bY[NT][2];
+    issue(0, 0);
+    if (KS > 1) issue(1, 1);
+    load_b(0, bX);
+    __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0), as in the LDS path
     lds_barrier();
-    if (ks + 2 < KS) issue(ks + 2, (ks + 2) % NSTAGE);
-    compute(ks % NSTAGE, (ks + 1) % NSTAGE);
+    read_a(0, 0, a0);
+    for (int ks = 0; ks < KS; ks += 2) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+      lds_barrier();
+      if (ks + 2 < KS) issue(ks + 2, (ks + 2) % NSTAGE);
+      if (ks + 1 < KS) {
+        load_b(ks + 1, bY);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) bY[j][0] = bY[j][1] = make_uint4(0, 0, 0, 0);
+      }
+      compute(ks % NSTAGE, (ks + 1) % NSTAGE, bX);
+      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+      lds_barrier();
+      if (ks + 3 < KS) issue(ks + 3, (ks + 3) % NSTAGE);
+      if (ks + 2 < KS) load_b(ks + 2, bX);
+      compute((ks + 1) % NSTAGE, (ks + 2) % NSTAGE, bY);
+    }
+  } else {
+    // Fragments of k-step s of the stage in LDS buffer st (weights, activations).
+    auto read = [&](int st, int s, uint4 (&bw)[NT], uint4 (&av)[MT]) {
+      const uint8_t* base = lds + st * STAGE;
+      const uint32_t col = (uint32_t)(((2 * s + h) ^ fl) * 16);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        bw[j] = *reinterpret_cast<const uint4*>(base + A_BYTES + (64 * wave + 32 * j + l32) * 64 + col);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) av[i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 64 + col);
+    };
+    auto mfmas = [&](const uint4 (&bw)[NT], const uint4 (&av)[MT]) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bw[j]),
+                                                            __builtin_bit_cast(i32x4, av[i]), acc[j][i], 0, 0, 0);
+    };
+    // One stage (buffer st).  On entry b0 / a0 hold its k-step 0 fragments.
+    // Step 0 issues the reads of step 1, then its MFMAs; step 1 issues the
+    // reads of the NEXT stage's k-step 0 (buffer nst), then its MFMAs, so no
+    // stage starts with its MFMAs waiting behind the barrier for LDS reads.
+    // The fences keep the compiler from sinking each read next to its use.
+    uint4 b0[NT], a0[MT];
+    auto compute = [&](int st, int nst) {
+      uint4 b1[NT], a1[MT];
+      read(st, 1, b1, a1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(b0, a0);
+      __builtin_amdgcn_sched_barrier(0);
+      read(nst, 0, b0, a0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(b1, a1);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Stage ks uses buffer ks % 3.  At its top: vmcnt(0) lands this wave's
+    // copies of stage ks + 1 (issued one stage earlier), and the barrier makes
+    // every wave's visible and guarantees every wave is done with buffer
+    // (ks + 2) % 3 = the previous stage's, which then receives stage ks + 2.
+    // Stages past KS - 1 are not copied; the last stage's read of the "next"
+    // stage reads a buffer nobody uses again (its values are dropped).
+    issue(0, 0);
+    if (KS > 1) issue(1, 1);
+    // vmcnt(0): stages 0 and 1; lgkmcnt(0), as a builtin the compiler sees:
+    // a scalar load it hoisted here (a kernel argument of the epilogue) would
+    // otherwise count as pending through the loop, and since scalar loads
+    // return out of order the compiler would wait lgkmcnt(0) for every LDS read
+    __builtin_amdgcn_s_waitcnt(0x0070);
+    lds_barrier();
+    read(0, 0, b0, a0);
+    for (int ks = 0; ks < KS; ++ks) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+      lds_barrier();
+      if (ks + 2 < KS) issue(ks + 2, (ks + 2) % NSTAGE);
+      compute(ks % NSTAGE, (ks + 1) % NSTAGE);
+    }
   }
 
   if constexpr (OUT == 2) {
@@ -203,8 +294,6 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
     // fp16 output: the wave's BM x 64 tile is staged in LDS (reusing the
     // pipeline buffers) and written back as whole 128-byte rows.
     lds_barrier();  // every wave is done reading the pipeline stages
-    constexpr int EP = 128;  // bytes per staged row (64 fp16, chunk-swizzled: stg_off)
-    static_assert(4 * BM * EP <= NSTAGE * STAGE, "epilogue staging fits in the pipeline LDS");
     uint8_t* stg = lds + wave * (BM * EP);
     float am[MT];
 #pragma unroll
@@ -297,6 +386,27 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
   }
 }
 
+// Re-layout of an N x K int8 weight for the PACKED kernel: 16-byte chunk
+// ((cb * KS + ks) * 2 + s) * 64 + L of the output is bytes
+// [64 ks + 32 s + 16 (L / 32), +16) of row 32 cb + L % 32 (zeros for rows past
+// N, which is rounded up to 32).  One thread per output chunk.
+__global__ __launch_bounds__(256) void w8a8_pack_kernel(const int8_t* __restrict__ w, int8_t* __restrict__ p,
+                                                        int N, int K, long nchunks) {
+  const long c = (long)blockIdx.x * 256 + threadIdx.x;
+  if (c >= nchunks) return;
+  const int KS = K >> 6;
+  const int L = (int)(c & 63);
+  const long blk = c >> 6;                  // (cb * KS + ks) * 2 + s
+  const int s = (int)(blk & 1);
+  const long cbks = blk >> 1;
+  const int ks = (int)(cbks % KS);
+  const int cb = (int)(cbks / KS);
+  const int n = 32 * cb + (L & 31);
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (n < N) v = *reinterpret_cast<const uint4*>(w + (size_t)n * K + 64 * ks + 32 * s + 16 * (L >> 5));
+  *reinterpret_cast<uint4*>(p + c * 16) = v;
+}
+
 // Width (in 256-column tiles) of the column groups the tile order walks.  A
 // read model per launch: every column group reads all of A once (its rows
 // are shared by the gn tiles of a row, which run side by side on one XCD),
@@ -322,25 +432,28 @@ static int w8a8_col_group(long tiles_m, int tiles_n, long M, long K) {
   return best;
 }
 
-template <int MT, int OUT>
+template <int MT, int OUT, bool PACKED>
 static void launch(const void* a, const void* b, const void* ws, const void* as, const void* bias,
                    const void* gamma, void* out, int M, int N, int K, hipStream_t st) {
   const int tiles_m = (M + 32 * MT - 1) / (32 * MT), tiles_n = (N + 255) / 256;
   const int gn = w8a8_col_group(tiles_m, tiles_n, M, K);
-  hipLaunchKernelGGL((w8a8_gemm_kernel<MT, OUT>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
+  hipLaunchKernelGGL((w8a8_gemm_kernel<MT, OUT, PACKED>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
                      (const int8_t*)a, (const int8_t*)b, (const uint16_t*)ws, (const uint16_t*)as,
                      (const uint16_t*)bias, (const uint16_t*)gamma, out, M, N, K, tiles_n, gn);
 }
 
 // mode: 0 = fp16 out, 1 = fp16 out + bias, 2 = int32 accumulators,
-// 3 = bias + LayerScale residual into `out` (the residual stream)
+// 3 = bias + LayerScale residual into `out` (the residual stream);
+// packed: b is the qv_w8a8_pack_weight layout (modes 0, 1, 3)
 static int w8a8_run(const void* a, const void* b, const void* ws, const void* as, const void* bias,
-                    const void* gamma, void* out, int64_t M, int64_t N, int64_t K, int mode, void* stream) {
+                    const void* gamma, void* out, int64_t M, int64_t N, int64_t K, int mode, void* stream,
+                    bool packed = false) {
   QV_CHECK_ARG(M >= 0 && N > 0 && K > 0, "bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   QV_CHECK_ARG(K % 64 == 0, "K=%lld must be a multiple of 64", (long long)K);
   QV_CHECK_ARG(N % 16 == 0, "N=%lld must be a multiple of 16", (long long)N);
   QV_CHECK_ARG(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "shape too large");
-  QV_CHECK_ARG((uint64_t)N * K < (1ull << 32) && (uint64_t)128 * K < (1ull << 31), "weight too large for 32-bit offsets");
+  QV_CHECK_ARG((uint64_t)((N + 31) & ~31) * K < (1ull << 32) && (uint64_t)128 * K < (1ull << 31),
+               "weight too large for 32-bit offsets");
   if (M == 0) return QV_OK;
   QV_CHECK_ARG(a && b && out && (mode == 2 || (ws && as)) && ((mode != 1 && mode != 3) || bias) &&
                    (mode != 3 || gamma),
@@ -353,17 +466,20 @@ static int w8a8_run(const void* a, const void* b, const void* ws, const void* as
   hipStream_t st = (hipStream_t)stream;
   const long big_tiles = (long)((M + 127) / 128) * ((N + 255) / 256);
   const bool big = big_tiles >= 256;
-#define QV_W8(MT)                                                                               \
-  switch (mode) {                                                                               \
-    case 0: launch<MT, 0>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;   \
-    case 1: launch<MT, 1>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;   \
-    case 3: launch<MT, 3>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;   \
-    default: launch<MT, 2>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;  \
+  QV_CHECK_ARG(!packed || mode != 2, "the packed weight layout has no int32 output");
+#define QV_W8(MT, P)                                                                                \
+  switch (mode) {                                                                                   \
+    case 0: launch<MT, 0, P>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;    \
+    case 1: launch<MT, 1, P>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;    \
+    case 3: launch<MT, 3, P>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); break;    \
+    default:                                                                                        \
+      if constexpr (!P) launch<MT, 2, P>(a, b, ws, as, bias, gamma, out, (int)M, (int)N, (int)K, st); \
+      break;                                                                                        \
   }
   if (big) {
-    QV_W8(4)
+    if (packed) { QV_W8(4, true) } else { QV_W8(4, false) }
   } else {
-    QV_W8(2)
+    if (packed) { QV_W8(2, true) } else { QV_W8(2, false) }
   }
 #undef QV_W8
   return check_launch("w8a8_gemm");
@@ -385,4 +501,27 @@ extern "C" int qv_w8a8_gemm_residual(const int8_t* a, const int8_t* b, const voi
 extern "C" int qv_w8a8_gemm_i32(const int8_t* a, const int8_t* b, int32_t* out, int64_t M, int64_t N, int64_t K,
                                 void* stream) {
   return qv::w8a8_run(a, b, nullptr, nullptr, nullptr, nullptr, out, M, N, K, 2, stream);
+}
+
+extern "C" int64_t qv_w8a8_packed_bytes(int64_t N, int64_t K) {
+  return N > 0 && K > 0 ? (N + 31) / 32 * 32 * K : 0;
+}
+
+extern "C" int qv_w8a8_pack_weight(const int8_t* w, int8_t* packed, int64_t N, int64_t K, void* stream) {
+  QV_CHECK_ARG(N > 0 && K > 0 && K % 64 == 0 && N % 16 == 0,
+               "bad weight shape N=%lld K=%lld (K a multiple of 64, N of 16)", (long long)N, (long long)K);
+  QV_CHECK_ARG((uint64_t)((N + 31) & ~31) * K < (1ull << 32), "weight too large for 32-bit offsets");
+  QV_CHECK_ARG(w && packed, "null pointer argument");
+  QV_CHECK_ARG(((uintptr_t)w % 16) == 0 && ((uintptr_t)packed % 16) == 0, "w and packed must be 16-byte aligned");
+  const long nchunks = (long)((N + 31) / 32) * (K / 64) * 2 * 64;
+  hipLaunchKernelGGL(qv::w8a8_pack_kernel, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, w, packed, (int)N, (int)K, nchunks);
+  return qv::check_launch("w8a8_pack_weight");
+}
+
+extern "C" int qv_w8a8_gemm_packed(const int8_t* a, const int8_t* packed_b, const void* wscales,
+                                   const void* ascales, const void* bias, const void* gamma, void* out, int64_t M,
+                                   int64_t N, int64_t K, void* stream) {
+  return qv::w8a8_run(a, packed_b, wscales, ascales, bias, gamma, out, M, N, K, gamma ? 3 : (bias ? 1 : 0), stream,
+                      true);
 }

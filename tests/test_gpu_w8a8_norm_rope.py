@@ -123,6 +123,85 @@ def test_w8a8_linear_residual_bit_exact(gpu, M, N, K):
     assert np.array_equal(_bits(resid), ref.view(np.int16))
 
 
+# ------------------------------------------------------ packed weights
+def _pack_mirror(b: np.ndarray) -> np.ndarray:
+    """The packed layout from its definition: 16-byte chunk
+    ((cb * KS + ks) * 2 + s) * 64 + L = bytes [64 ks + 32 s + 16 (L // 32), +16)
+    of row 32 cb + L % 32, rows past N zero."""
+    N, K = b.shape
+    KS, CB = K // 64, (N + 31) // 32
+    bp = np.zeros((CB * 32, K), np.int8)
+    bp[:N] = b
+    # (cb, r, ks, s, half, 16) -> (cb, ks, s, half, r, 16): lane L = 32 half + r
+    v = bp.reshape(CB, 32, KS, 2, 2, 16).transpose(0, 2, 3, 4, 1, 5)
+    return np.ascontiguousarray(v).reshape(-1)
+
+
+@pytest.mark.parametrize("N,K", [(4096, 1024), (272, 192), (48, 64)])
+def test_w8a8_pack_weight_layout(gpu, N, K):
+    from qvggt_amd import awq_inference_engine as E
+    b = _rng(N + K).integers(-128, 128, (N, K)).astype(np.int8)
+    p = E.w8a8_pack_weight(torch.from_numpy(b).to(gpu))
+    assert p.numel() == E.w8a8_packed_bytes(N, K) == (N + 31) // 32 * 32 * K
+    assert np.array_equal(p.cpu().numpy(), _pack_mirror(b))
+
+
+# (37, 272, 192): three k stages (odd: the last loop iteration multiplies zero
+# weights) and N = 272, which the layout pads to 288; (50, 1040, 64) one stage;
+# (129, 1040, 320) five; (10992, 4096, 1024) and (10992, 1024, 4096) the
+# 128-row tiles of the benchmark's MLP pair; (4100, 4112, 1024) column groups
+# with a narrower last group.
+@pytest.mark.parametrize("mode", ["plain", "bias", "residual"])
+@pytest.mark.parametrize("M,N,K", [(10992, 4096, 1024), (10992, 1024, 4096), (1374, 3072, 1024), (37, 272, 192),
+                                   (50, 1040, 64), (129, 1040, 320), (4100, 4112, 1024)])
+def test_w8a8_gemm_packed_bit_exact(gpu, M, N, K, mode):
+    """qv_w8a8_gemm_packed against the oracle, as the unpacked GEMM is held."""
+    from qvggt_amd import awq_inference_engine as E
+    rng = _rng(M * 3 + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    a, as_ = Q.quant_per_token(x)
+    b = np.clip(np.rint(rng.standard_normal((N, K)) * 32), -128, 127).astype(np.int8)
+    ws = rng.uniform(0.0005, 0.005, N).astype(np.float16)
+    bb = (rng.standard_normal(N) * 0.1).astype(np.float16) if mode != "plain" else None
+    g = rng.uniform(0.005, 1.5, N).astype(np.float16)
+    ta, tb, tws, tas = (torch.from_numpy(v).to(gpu) for v in (a, b, ws, as_))
+    tbb = torch.from_numpy(bb).to(gpu) if bb is not None else None
+    p = E.w8a8_pack_weight(tb)
+    o = Q.w8a8_epilogue(Q.w8a8_int32(a, b), ws, as_, bb)
+    if mode == "residual":
+        r0 = rng.standard_normal((M, N)).astype(np.float16)
+        out = torch.from_numpy(r0).to(gpu)
+        E.w8a8_gemm_packed(ta, p, N, tws, tas, out, bias=tbb, gamma=torch.from_numpy(g).to(gpu))
+        ref = (r0.astype(np.float32) + o.astype(np.float32) * g.astype(np.float32)).astype(np.float16)
+    else:
+        out = torch.empty(M, N, dtype=torch.float16, device=gpu)
+        E.w8a8_gemm_packed(ta, p, N, tws, tas, out, bias=tbb)
+        ref = o
+    assert np.array_equal(_bits(out), ref.view(np.int16))
+
+
+def test_w8a8_linear_repacks_a_changed_weight(gpu):
+    """W8A8Linear runs on a packed copy of its weight; writing the weight in
+    place must re-make the copy (the module's output follows the weight)."""
+    from qvggt_amd import aggregator as AG
+    rng = _rng(5)
+    M, N, K = 200, 512, 256
+    m = AG.W8A8Linear(K, N, bias=True, dev=gpu)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    a, as_ = Q.quant_per_token(x)
+    ta, tas = torch.from_numpy(a).to(gpu), torch.from_numpy(as_).to(gpu)
+    ws = rng.uniform(0.0005, 0.005, N).astype(np.float16)
+    bb = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    m.wscales.copy_(torch.from_numpy(ws))
+    m.bias.copy_(torch.from_numpy(bb))
+    for seed in (1, 2):
+        b = _rng(seed).integers(-128, 128, (N, K)).astype(np.int8)
+        m.weight.copy_(torch.from_numpy(b))
+        out = m(ta, tas)
+        ref = Q.w8a8_epilogue(Q.w8a8_int32(a, b), ws, as_, bb)
+        assert np.array_equal(_bits(out), ref.view(np.int16)), seed
+
+
 # ------------------------------------------------------- LN + quant
 @pytest.mark.parametrize("M,D,dt", [(10992, 1024, "f16"), (33, 4096, "f16"), (7, 1000, "f16"), (1001, 2048, "f16"), (18, 512, "f16"),
                                     (1374, 1024, "bf16"), (65, 4096, "bf16"), (300, 1024, "f32"), (9, 2048, "f32")])

@@ -86,6 +86,15 @@ def test_host_checks_reject_bad_shapes_before_any_launch():
             E.qknorm_rope2d(qkv, pos, c, s_, H, g, g, g, g)
         with pytest.raises(RuntimeError, match="tables|differ"):
             E.rope2d(qkv, pos, c, s_, H)
+    # a packed W8A8 weight whose size does not match (N, K)
+    a8 = torch.zeros(m, 128, dtype=torch.int8)
+    s8 = torch.zeros(m, dtype=torch.float16)
+    ws = torch.zeros(n, dtype=torch.float16)
+    o8 = torch.zeros(m, n, dtype=torch.float16)
+    assert E.w8a8_packed_bytes(n, 128) == 64 * 128 and E.w8a8_packed_bytes(48, 128) == 64 * 128
+    for bad in (torch.zeros(n * 128 - 16, dtype=torch.int8), torch.zeros(n, 128, dtype=torch.int8)):
+        with pytest.raises(RuntimeError, match="packed weight must be"):
+            E.w8a8_gemm_packed(a8, bad, n, ws, s8, o8)
 
 
 def test_ops_refuse_cpu_tensors_and_bad_dtypes():
