@@ -8,7 +8,7 @@
     python qvggt_amd/profiling.py dense M K N [--bias | --int8]
     python qvggt_amd/profiling.py sdpa [--frames S] [--global]
     python qvggt_amd/profiling.py rows [--reps R]
-    python qvggt_amd/profiling.py w8a8 M K N [--reps R]
+    python qvggt_amd/profiling.py w8a8 M K N [--reps R] [--packed]
     python qvggt_amd/profiling.py trace-summary KERNEL_TRACE_CSV [--match NAME] [--grid G] [--run RUN --last N]
     python qvggt_amd/profiling.py pmc-summary COUNTER_COLLECTION_CSV [--match NAME]
 
@@ -33,7 +33,8 @@ angles) on S = 32 tokens (43968 x 1024), GELU + quant on the MLP hidden (10992 x
 2-D RoPE and qk-norm + 2-D RoPE on the S = 32 qkv (43968 x 3072) -- R times,
 each launch on its own buffer set (so no launch finds its data in the
 caches).  ``w8a8`` runs the W8A8 GEMM with bias (int8 MFMA) on random int8
-operands.  Every mode above prints one line when done.
+operands (``--packed``: on the packed weight layout, packed before the
+timed launches).  Every mode above prints one line when done.
 
 ``trace-summary`` reads a rocprofv3 kernel-trace CSV and prints the dispatch
 count, mean and median duration of the kernels whose name contains NAME
@@ -211,7 +212,7 @@ def _rows(reps):
           f"qknorm_rope2d (S=32), {reps} launches each", flush=True)
 
 
-def _w8a8(M, K, N, reps):
+def _w8a8(M, K, N, reps, packed):
     import torch
 
     from qvggt_amd import awq_inference_engine as E
@@ -224,11 +225,15 @@ def _w8a8(M, K, N, reps):
     as_ = (torch.rand(M, generator=g) * 0.01).half().to(dev)
     b = torch.zeros(N, dtype=torch.float16, device=dev)
     o = torch.empty(M, N, dtype=torch.float16, device=dev)
+    wp = E.w8a8_pack_weight(w) if packed else None
     _prewarm()
     for _ in range(reps):
-        E.w8a8_gemm_fuse_bias_forward_cuda(a, w, ws, as_, o, b)
+        if packed:
+            E.w8a8_gemm_packed(a, wp, N, ws, as_, o, bias=b)
+        else:
+            E.w8a8_gemm_fuse_bias_forward_cuda(a, w, ws, as_, o, b)
     torch.cuda.synchronize()
-    print(f"w8a8: M={M} K={K} N={N} + bias, {reps} launches", flush=True)
+    print(f"w8a8: M={M} K={K} N={N} + bias{' (packed weights)' if packed else ''}, {reps} launches", flush=True)
 
 
 def _trace_summary(path, match, grid, run, last):
@@ -367,6 +372,7 @@ def main(argv=None):
     w.add_argument("K", type=int)
     w.add_argument("N", type=int)
     w.add_argument("--reps", type=int, default=3)
+    w.add_argument("--packed", action="store_true")
     ts = sub.add_parser("trace-summary")
     ts.add_argument("csv")
     ts.add_argument("--match", default="")
@@ -392,7 +398,7 @@ def main(argv=None):
     elif args.mode == "rows":
         _rows(args.reps)
     elif args.mode == "w8a8":
-        _w8a8(args.M, args.K, args.N, args.reps)
+        _w8a8(args.M, args.K, args.N, args.reps, args.packed)
     elif args.mode == "pmc-summary":
         _pmc_summary(args.csv, args.match)
     elif args.mode == "trace-summary":
