@@ -341,6 +341,33 @@ __global__ __launch_bounds__(256) void rope2d_kernel(const uint16_t* __restrict_
 // (DPP, no LDS); two-pass variance; one rounding per fp32 operation.  The
 // rotation partner of dim d (d +- 16 in its half) sits in lane j ^ 2.
 constexpr int QKN_ROWS_PER_WG = 32;  // 4 waves x 8 rows per row slot; NR slots per workgroup
+
+// q/k LayerNorm of one row's 8 values in a lane (packed fp16 xw, the row
+// spread over 8 lanes): mean, two-pass variance, affine, rounded to fp16 yw.
+__device__ __forceinline__ void qk_norm8(const uint32_t (&xw)[4], const uint4& g, const uint4& b, float eps,
+                                         uint32_t (&yw)[4]) {
+  float s = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    s = mix_add<0>(xw[m], s);
+    s = mix_add<1>(xw[m], s);
+  }
+  const float nm = -(sum8_lanes(s) / 64.0f);
+  float d[8], s2 = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    d[2 * m] = mix_add<0>(xw[m], nm);
+    d[2 * m + 1] = mix_add<1>(xw[m], nm);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s2 = s2 + d[e] * d[e];
+  const float rs = 1.0f / __builtin_sqrtf(sum8_lanes(s2) / 64.0f + eps);
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    yw[m] = pack2<false>(mix_add<0>(bw[m], mix_mul<0>(d[2 * m] * rs, gw[m])),
+                         mix_add<1>(bw[m], mix_mul<1>(d[2 * m + 1] * rs, gw[m])));
+}
 template <int NR>
 __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
     uint16_t* __restrict__ qkv, const int* __restrict__ pos, const float* __restrict__ cos_t,
@@ -386,38 +413,99 @@ __global__ __launch_bounds__(256) void qknorm_rope2d_kernel(
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
-    float s = 0.f;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      s = mix_add<0>(xw[k][m], s);
-      s = mix_add<1>(xw[k][m], s);
-    }
-    const float nm = -(sum8_lanes(s) / 64.0f);
-    float d[8], s2 = 0.f;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      d[2 * m] = mix_add<0>(xw[k][m], nm);
-      d[2 * m + 1] = mix_add<1>(xw[k][m], nm);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s2 = s2 + d[e] * d[e];
-    const float rs = 1.0f / __builtin_sqrtf(sum8_lanes(s2) / 64.0f + eps);
-    const uint4 g = partv[k] ? gk : gq;
-    const uint4 b = partv[k] ? bk : bq;
-    const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, bw[4] = {b.x, b.y, b.z, b.w};
-    uint32_t yw[4];   // q_norm / k_norm output, rounded to fp16
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-      yw[m] = pack2<false>(mix_add<0>(bw[m], mix_mul<0>(d[2 * m] * rs, gw[m])),
-                           mix_add<1>(bw[m], mix_mul<1>(d[2 * m + 1] * rs, gw[m])));
+    uint32_t yw[4];
+    qk_norm8(xw[k], partv[k] ? gk : gq, partv[k] ? bk : bq, eps, yw);
     const uint4 o = rotate8(yw, an[k], lo);
     if (live[k]) st_stream16(row[k] + 8 * j, o);
+  }
+}
+
+// Token blocks.  When H is a multiple of 16 a token's 2H rows are whole
+// 32-row blocks, so the 32 rows of one block share a token and its position
+// pair.  A wave takes one block: group g (lanes 8g .. 8g + 7) takes rows
+// g, g + 8, g + 16, g + 24 of it, and each lane loads its 8 cos / sin pairs
+// once for all four.  With the angles held once instead of per row, four rows
+// per lane are in flight at full occupancy (the per-row form holds two).
+// Results are those of the per-row kernels bit for bit (the same arithmetic
+// per row).
+constexpr int TOK_ROWS = 4;        // rows per 8-lane group
+constexpr int TOK_WAVES = 4;       // waves (32-row blocks) per workgroup
+
+__global__ __launch_bounds__(64 * TOK_WAVES) void rope2d_tok_kernel(
+    const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, const int* __restrict__ pos,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int P, int T, int H, long src_tok,
+    long dst_tok, long dst_part, int hshift) {
+  const long base = ((long)blockIdx.x * TOK_WAVES + (threadIdx.x >> 6)) * 32;
+  if (base >= (long)T * 2 * H) return;   // whole block past the end (wave-uniform; no barriers)
+  const int g = (threadIdx.x >> 3) & 7, j = threadIdx.x & 7;
+  const int half = j >> 2, i0 = 8 * (j & 1);
+  const bool lo = (j & 2) == 0;
+  int tok, part0, head0;
+  row_coords(base, H, hshift, tok, part0, head0);
+  const int rr0 = part0 * H + head0 + g;   // row of the token (q heads, then k heads)
+  const int pv = pos[2 * tok + half];
+  const uint16_t* s0 = src + (size_t)tok * src_tok + 8 * j;
+  uint32_t xw[TOK_ROWS][4];
+#pragma unroll
+  for (int k = 0; k < TOK_ROWS; ++k) {
+    const uint4 v = ld_stream16(s0 + (size_t)(rr0 + 8 * k) * 64);
+    xw[k][0] = v.x; xw[k][1] = v.y; xw[k][2] = v.z; xw[k][3] = v.w;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const Angles8 an = load_angles(cos_t, sin_t, pv, P, i0);
+  __builtin_amdgcn_sched_barrier(0);
+  uint16_t* d0 = dst + (size_t)tok * dst_tok + 8 * j;
+#pragma unroll
+  for (int k = 0; k < TOK_ROWS; ++k) {
+    const int rr = rr0 + 8 * k;
+    const int part = rr >= H;
+    const int head = rr - (part ? H : 0);
+    st_stream16(d0 + (size_t)part * dst_part + (size_t)head * 64, rotate8(xw[k], an, lo));
+  }
+}
+
+__global__ __launch_bounds__(64 * TOK_WAVES) void qknorm_rope2d_tok_kernel(
+    uint16_t* __restrict__ qkv, const int* __restrict__ pos, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int P, const uint16_t* __restrict__ qg, const uint16_t* __restrict__ qb,
+    const uint16_t* __restrict__ kg, const uint16_t* __restrict__ kb, float eps, int T, int H, long tok_stride,
+    int hshift) {
+  const long base = ((long)blockIdx.x * TOK_WAVES + (threadIdx.x >> 6)) * 32;
+  if (base >= (long)T * 2 * H) return;   // whole block past the end (wave-uniform; no barriers)
+  const int g = (threadIdx.x >> 3) & 7, j = threadIdx.x & 7;
+  const int half = j >> 2, i0 = 8 * (j & 1);
+  const bool lo = (j & 2) == 0;
+  int tok, part0, head0;
+  row_coords(base, H, hshift, tok, part0, head0);
+  const int rr0 = part0 * H + head0 + g;
+  const int pv = pos[2 * tok + half];
+  uint16_t* r0 = qkv + (size_t)tok * tok_stride + 8 * j;
+  uint32_t xw[TOK_ROWS][4];
+#pragma unroll
+  for (int k = 0; k < TOK_ROWS; ++k) {
+    const uint4 v = ld_stream16(r0 + (size_t)(rr0 + 8 * k) * 64);
+    xw[k][0] = v.x; xw[k][1] = v.y; xw[k][2] = v.z; xw[k][3] = v.w;
+  }
+  const uint4 gq = reinterpret_cast<const uint4*>(qg)[j], bq = reinterpret_cast<const uint4*>(qb)[j];
+  const uint4 gk = reinterpret_cast<const uint4*>(kg)[j], bk = reinterpret_cast<const uint4*>(kb)[j];
+  __builtin_amdgcn_sched_barrier(0);
+  const Angles8 an = load_angles(cos_t, sin_t, pv, P, i0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < TOK_ROWS; ++k) {
+    const int rr = rr0 + 8 * k;
+    const bool kpart = rr >= H;
+    uint32_t yw[4];
+    qk_norm8(xw[k], kpart ? gk : gq, kpart ? bk : bq, eps, yw);
+    st_stream16(r0 + (size_t)rr * 64, rotate8(yw, an, lo));
   }
 }
 
 }  // namespace qv
 
 using namespace qv;
+
+// the token-block kernels' grid: one wave per 32 rows, a 32-bit workgroup count
+static bool tok_blocks_ok(long rows) { return rows / 32 / TOK_WAVES < INT32_MAX; }
 
 extern "C" int qv_qknorm_rope2d(void* qkv, const int32_t* positions, const float* cos_table, const float* sin_table,
                                 int64_t table_rows, const void* q_gamma, const void* q_beta, const void* k_gamma,
@@ -435,13 +523,21 @@ extern "C" int qv_qknorm_rope2d(void* qkv, const int32_t* positions, const float
                "tables and norm weights must be 16-byte aligned");
   const long rows = T * 2 * H;
   QV_CHECK_ARG(rows / QKN_ROWS_PER_WG < INT32_MAX, "too many rows");
+  const int hshift = (H & (H - 1)) == 0 ? __builtin_ctzll((unsigned long long)H) : -1;
+  if (H % 16 == 0 && tok_blocks_ok(rows)) {
+    hipLaunchKernelGGL(qknorm_rope2d_tok_kernel, dim3((unsigned)((rows / 32 + TOK_WAVES - 1) / TOK_WAVES)),
+                       dim3(64 * TOK_WAVES), 0, (hipStream_t)stream, (uint16_t*)qkv, positions, cos_table,
+                       sin_table, (int)table_rows, (const uint16_t*)q_gamma, (const uint16_t*)q_beta,
+                       (const uint16_t*)k_gamma, (const uint16_t*)k_beta, eps, (int)T, (int)H, (long)token_stride,
+                       hshift);
+    return check_launch("qknorm_rope2d");
+  }
   constexpr int NR = 2;   // two rows per 8-lane group: 3 % faster than one at S = 32
   hipLaunchKernelGGL(qknorm_rope2d_kernel<NR>,
                      dim3((unsigned)((rows + QKN_ROWS_PER_WG * NR - 1) / (QKN_ROWS_PER_WG * NR))), dim3(256), 0,
                      (hipStream_t)stream, (uint16_t*)qkv, positions, cos_table, sin_table, (int)table_rows,
                      (const uint16_t*)q_gamma, (const uint16_t*)q_beta, (const uint16_t*)k_gamma,
-                     (const uint16_t*)k_beta, eps, (int)T, (int)H, (long)token_stride,
-                     (H & (H - 1)) == 0 ? __builtin_ctzll((unsigned long long)H) : -1);
+                     (const uint16_t*)k_beta, eps, (int)T, (int)H, (long)token_stride, hshift);
   return check_launch("qknorm_rope2d");
 }
 
@@ -496,12 +592,20 @@ extern "C" int qv_rope2d(const void* qkv, void* out, const int32_t* positions, c
                    ((uintptr_t)qkv % 16) == 0 && ((uintptr_t)out % 16) == 0 && ((uintptr_t)cos_table % 16) == 0 &&
                    ((uintptr_t)sin_table % 16) == 0,
                "rope2d needs 16-byte aligned rows and tables");
+  const long nrows = T * 2 * H;
+  const int hshift = (H & (H - 1)) == 0 ? __builtin_ctzll((unsigned long long)H) : -1;
+  if (H % 16 == 0 && tok_blocks_ok(nrows)) {
+    hipLaunchKernelGGL(rope2d_tok_kernel, dim3((unsigned)((nrows / 32 + TOK_WAVES - 1) / TOK_WAVES)),
+                       dim3(64 * TOK_WAVES), 0, (hipStream_t)stream, (const uint16_t*)qkv, (uint16_t*)out, positions,
+                       cos_table, sin_table, (int)table_rows, (int)T, (int)H, (long)src_token_stride,
+                       (long)dst_token_stride, (long)dst_part_stride, hshift);
+    return check_launch("rope2d");
+  }
   // two rows per 8-lane group: 10 % faster than one at S = 32, four no better
   constexpr int NR = 2;
-  const long nrows = T * 2 * H;
   hipLaunchKernelGGL(rope2d_kernel<NR>, dim3((unsigned)((nrows + 32 * NR - 1) / (32 * NR))), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)qkv, (uint16_t*)out, positions, cos_table, sin_table,
                      (int)table_rows, (int)T, (int)H, (long)src_token_stride, (long)dst_token_stride,
-                     (long)dst_part_stride, (H & (H - 1)) == 0 ? __builtin_ctzll((unsigned long long)H) : -1);
+                     (long)dst_part_stride, hshift);
   return check_launch("rope2d");
 }

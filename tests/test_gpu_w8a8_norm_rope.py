@@ -496,12 +496,14 @@ def test_fused_rope_with_pos(gpu, transpose_out, dt, shape):
         assert np.abs(got - ref).max() <= 2e-6 * max(1.0, np.abs(ref).max())
 
 
-@pytest.mark.parametrize("inplace,H", [(False, 16), (True, 16), (False, 6), (True, 1)])
-def test_rope2d_bit_exact(gpu, inplace, H):
-    """H = 16 (a power of two) takes the kernel's shift-based row indexing,
-    H = 6 the division path; H = 1 is the smallest power of two."""
+@pytest.mark.parametrize("inplace,H,S", [(False, 16, 2), (True, 16, 2), (False, 6, 2), (True, 1, 2), (False, 48, 1),
+                                         (True, 32, 1)])
+def test_rope2d_bit_exact(gpu, inplace, H, S):
+    """H a multiple of 16 takes the token-block kernel (H = 48: the q / k
+    boundary inside a 32-row block; S = 1: a last workgroup with idle
+    waves), other H the per-row kernel; H = 16 and 1 (powers of two) index
+    rows by shifts, H = 6 and 48 by division."""
     from qvggt_amd import awq_inference_engine as E
-    S = 2
     pos = R.vggt_positions(S)
     T = pos.shape[0]
     qkv = _rng(4).standard_normal((T, 3 * H * 64)).astype(np.float16)
@@ -522,10 +524,11 @@ def test_rope2d_bit_exact(gpu, inplace, H):
         assert np.array_equal(got[:, part].view(np.int16), ref.view(np.int16))
 
 
-@pytest.mark.parametrize("H", [16, 6])
-def test_qknorm_rope2d_bit_exact(gpu, H):
+@pytest.mark.parametrize("H,S", [(16, 2), (6, 2), (48, 1), (32, 1)])
+def test_qknorm_rope2d_bit_exact(gpu, H, S):
+    """H = 16, 48, 32: the token-block kernel (q and k rows in one 32-row
+    block at 16 and 48); H = 6: the per-row kernel."""
     from qvggt_amd import awq_inference_engine as E
-    S = 2
     pos = R.vggt_positions(S)
     T = pos.shape[0]
     rng = _rng(11)
