@@ -179,3 +179,24 @@ def test_patch_projection_equals_the_convolution():
     got = pe.project(img)
     assert got.shape == (2, AG.GRID * AG.GRID, AG.DIM)
     assert torch.allclose(got, ref, rtol=1e-12, atol=1e-10)
+
+
+def test_tanh_table_lookup_on_every_fp16_pattern():
+    """The GELU+quant kernel's tanh step, restated on all 65536 fp16 patterns
+    w: m = w & 0x7FFF, k = min(max(m - base, 0), last), t = min(m, table[k])
+    | (w & 0x8000), against fp16(fp32(tanh)) of the float64 value (NaN
+    patterns give +-1.0 by design: the GELU multiplies by its NaN input)."""
+    from qvggt_amd import build
+
+    base, last, table = build.tanh_f16_table()
+    assert table.dtype == np.uint16 and len(table) % 8 == 0 and table[last] == 0x3C00
+    w = np.arange(0x10000, dtype=np.uint32)
+    m = (w & 0x7FFF).astype(np.int64)
+    k = np.clip(m - base, 0, last)
+    got = (np.minimum(m, table[k].astype(np.int64)) | (w & 0x8000)).astype(np.uint16)
+    with np.errstate(invalid="ignore"):
+        want = np.tanh(w.astype(np.uint16).view(np.float16).astype(np.float64)).astype(np.float32)
+    want = want.astype(np.float16).view(np.uint16)
+    nan = m > 0x7C00
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all((got[nan] & 0x7FFF) == 0x3C00)
