@@ -34,6 +34,7 @@ SIGNATURES: dict[str, list] = {
     "qv_w4a16_dequant": [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp],
     "qv_w4a16_pack": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp],
     "qv_w4a16_gemm_residual": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    "qv_w4a16_plan": [_i64, _i64, _i64, _i32, _vp],
     "qv_w4a16_gemm_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp],
     "qv_w4a16_gemm_qkrope": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64,
                              _vp, _vp, _vp, _vp, _f32, _i64, _vp],

@@ -240,6 +240,18 @@ def w4a16_linear_residual(x: torch.Tensor, qweight: torch.Tensor, scales: torch.
     return residual
 
 
+def w4a16_plan(M: int, N: int, K: int, epilogue: int = _lib.QV_EPI_NONE) -> dict:
+    """The launch plan of an M x K -> N W4A16 linear (no device work):
+    ``kernel`` "skinny", "stream" or "stream_ksplit" (K summed in two halves
+    by two wave groups of one workgroup), ``tile`` rows of the first range,
+    ``rows`` the rows it covers, ``tile2`` the second range's tile height
+    (0: one range)."""
+    plan = (C.c_int32 * 4)()
+    _lib.call("qv_w4a16_plan", int(M), int(N), int(K), int(epilogue), C.cast(plan, C.c_void_p))
+    kind = {0: "skinny", 1: "stream", 2: "stream_ksplit"}[plan[0]]
+    return {"kernel": kind, "tile": plan[1], "rows": plan[2], "tile2": plan[3]}
+
+
 def gemm_forward_cuda_new(in_feats: torch.Tensor, kernel: torch.Tensor, scales: torch.Tensor,
                           zeros: torch.Tensor) -> torch.Tensor:
     """out[..., N] = in_feats[..., K] @ dequant(kernel)^T; N = kernel.size(0) * 4.

@@ -520,13 +520,26 @@ StreamPlan w4_stream_plan(int M, int N, int K, bool gelu) {
   return p;
 }
 
+#ifndef QV_W4_KSPLIT
+#define QV_W4_KSPLIT 1
+#endif
 StreamPlan w4_plan_for(int tile, int M, int N, int K, int epi) {
   StreamPlan p;
   if (tile == 6) {  // a grid of at most one tile per CU: the 32-row tile
     p.mt_a = 1;
-    return p;
+  } else {
+    p = w4_stream_plan(M, N, K, epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU);
   }
-  return w4_stream_plan(M, N, K, epi == QV_EPI_BIAS_GELU || epi == QV_EPI_GELU);
+  // One range of at most one tile per CU runs one wave per SIMD: split K
+  // between two 4-wave groups of one workgroup (whole 128-k groups each)
+  // where that measured faster -- long K (K >= 2048: M = 1374 and 2748 at
+  // 4096 -> 1024, -14 %) and the 32-row tile (1374 x 1024 -> 1024, -6 %).
+  // At K = 1024 with taller tiles the two groups, held in step by the
+  // shared per-stage barriers, wait on their loads together and the split
+  // measured 2-4 % slower (config 1: 14.67 -> 14.98 us).
+  const long tiles = (long)((M + 32 * p.mt_a - 1) / (32 * p.mt_a)) * ((N + 255) / 256);
+  p.ksplit = QV_W4_KSPLIT && p.mt_b == 0 && tiles <= 256 && K % 256 == 0 && (K >= 2048 || p.mt_a == 1);
+  return p;
 }
 }  // namespace
 
@@ -922,6 +935,26 @@ extern "C" int qv_w4a16_gemm_qkrope(const void* x, const void* qweight, const vo
   return launch_w4a16_stream<false>(x, qweight, scales, scaled_zeros, bias, nullptr, out, (int)M, (int)N, (int)K,
                                     QV_EPI_QKROPE, w4_plan_for(tile, (int)M, (int)N, (int)K, QV_EPI_QKROPE),
                                     (hipStream_t)stream, &a);
+}
+
+extern "C" int qv_w4a16_plan(int64_t M, int64_t N, int64_t K, int epilogue, int32_t* plan) {
+  QV_CHECK_ARG(plan != nullptr, "null plan pointer");
+  QV_CHECK_ARG(M > 0 && N > 0 && K > 0 && K % 128 == 0 && N % 16 == 0 && M <= INT32_MAX && N <= INT32_MAX &&
+                   K <= INT32_MAX,
+               "bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  QV_CHECK_ARG(epilogue >= QV_EPI_NONE && epilogue <= QV_EPI_GELU, "bad epilogue %d", epilogue);
+  const int tile = w4_pick_tile((int)M, (int)N, (int)K);
+  if (tile == 5) {
+    plan[0] = 0;
+    plan[1] = plan[2] = plan[3] = 0;
+    return QV_OK;
+  }
+  const StreamPlan p = w4_plan_for(tile, (int)M, (int)N, (int)K, epilogue);
+  plan[0] = p.ksplit ? 2 : 1;
+  plan[1] = 32 * p.mt_a;
+  plan[2] = p.mt_b ? p.rows_a : (int32_t)M;
+  plan[3] = 32 * p.mt_b;
+  return QV_OK;
 }
 
 extern "C" int qv_w4a16_gemm_noalloc(const void* x, const void* qweight, const void* scales,

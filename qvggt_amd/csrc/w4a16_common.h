@@ -151,6 +151,7 @@ __device__ __forceinline__ void epilogue_apply4v(const uint2& b, float (&r)[4]) 
 // 32 mt_a.
 struct StreamPlan {
   int mt_a = 4, rows_a = 0, mt_b = 0;
+  bool ksplit = false;   // one range of mt_a tiles, K split between two 4-wave groups
 };
 
 // Streamed (LDS-pipelined, 32x32 MFMA) GEMM, tiles (32 mt) x 256.

@@ -53,9 +53,11 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   // threadIdx.x through an empty asm: the lane-dependent addresses below are
   // then computed here, not hoisted out of a caller's loop over tiles and
   // kept live across it (in a kernel that loops over tiles, that hoisting
-  // made the accumulators spill)
+  // made the accumulators spill).  The index within the 4-wave group: the
+  // K-split kernel runs two such groups in one workgroup.
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
+  tid &= 255;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int h = lane >> 5, l32 = lane & 31;
@@ -439,6 +441,115 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
   }
 }
 
+// K split inside the workgroup, for launches of at most one tile per CU
+// (where the 4-wave kernel runs one wave per SIMD and nothing hides a wave's
+// own LDS, dequantisation and barrier latencies behind another's MFMAs).
+// Eight waves: group g = wave / 4 runs the main loop of the 4-wave kernel
+// over stages [g K/128, (g + 1) K/128) in its own three LDS stage buffers, so
+// each SIMD holds one wave of each group.  Then group 1 hands its fp32
+// partial sums to group 0 through LDS (one 16-byte slot per lane and
+// register quad: contiguous 1 KB per wave instruction), group 0 adds them
+// (its own first-half sum + the second half's) and runs the epilogue of the
+// 4-wave kernel.  Both groups run the same number of stages, so every
+// per-stage barrier of the main loop is reached by all eight waves; group 1
+// also takes part in the epilogue's opening barrier, after which it is done.
+template <int MT>
+constexpr int ksplit_lds_bytes() {
+  constexpr int stages = 2 * 3 * 32 * MT * 128, part = 32 * MT * 256 * 4, stage_out = 4 * 32 * MT * EP;
+  return stages > part ? (stages > stage_out ? stages : stage_out) : (part > stage_out ? part : stage_out);
+}
+
+template <bool BF16, int MT, int EPI>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void w4a16_ksplit_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
+                         const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
+                         const uint16_t* __restrict__ bias, const uint16_t* __restrict__ gamma,
+                         uint16_t* __restrict__ out, int M, int N, int K, int tiles_n, QkRopeArgs qk) {
+  constexpr int BM = 32 * MT;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[ksplit_lds_bytes<MT>()];
+  const int grp = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+  const int lid = xcd_remap(blockIdx.x, (int)gridDim.x);
+  const int m0 = (lid / tiles_n) * BM;
+  const int n0 = (lid % tiles_n) * 256;
+  const int half = K >> 7;   // stages per group (K % 256 == 0: an even count)
+  f32x16 acc[2][MT];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+  stream_mainloop<BF16, MT>(lds + grp * (3 * BM * 128), x, qw, scales, zeros, M, N, K, m0, n0, grp * half,
+                            (grp + 1) * half, acc);
+  // every wave is done reading its group's stage buffers
+  lds_barrier();
+  const int lane = threadIdx.x & 63;
+  const int wv = (threadIdx.x >> 6) & 3;
+  float4* part = reinterpret_cast<float4*>(lds) + (wv * (2 * MT * 4)) * 64 + lane;
+  if (grp == 1) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          part[((j * MT + i) * 4 + q) * 64] =
+              make_float4(acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
+  }
+  lds_barrier();
+  if (grp == 0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 p = part[((j * MT + i) * 4 + q) * 64];
+          acc[j][i][4 * q] += p.x;
+          acc[j][i][4 * q + 1] += p.y;
+          acc[j][i][4 * q + 2] += p.z;
+          acc[j][i][4 * q + 3] += p.w;
+        }
+    // its opening barrier (matched by group 1 below) also orders these
+    // reads before the staging writes that reuse the same LDS
+    stream_epilogue<BF16, MT, EPI>(lds, bias, gamma, out, M, N, qk, m0, n0, acc);
+  } else {
+    lds_barrier();
+  }
+}
+
+template <bool BF16, int MT>
+static void launch_ksplit(const void* x, const void* qw, const void* s, const void* z, const void* bias,
+                          const void* gamma, void* out, int M, int N, int K, int epi, hipStream_t st,
+                          const QkRopeArgs& qk) {
+  const int tiles_n = (N + 255) / 256;
+  const dim3 grid((M + 32 * MT - 1) / (32 * MT) * tiles_n), block(512);
+#define QV_ARGS                                                                                \
+  (const uint16_t*)x, (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,             \
+      (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, tiles_n, qk
+  switch (epi) {
+    case QV_EPI_NONE:
+      hipLaunchKernelGGL((w4a16_ksplit_kernel<BF16, MT, QV_EPI_NONE>), grid, block, 0, st, QV_ARGS);
+      break;
+    case QV_EPI_BIAS:
+      hipLaunchKernelGGL((w4a16_ksplit_kernel<BF16, MT, QV_EPI_BIAS>), grid, block, 0, st, QV_ARGS);
+      break;
+    case QV_EPI_BIAS_GELU:
+      hipLaunchKernelGGL((w4a16_ksplit_kernel<BF16, MT, QV_EPI_BIAS_GELU>), grid, block, 0, st, QV_ARGS);
+      break;
+    case QV_EPI_GELU:
+      hipLaunchKernelGGL((w4a16_ksplit_kernel<BF16, MT, QV_EPI_GELU>), grid, block, 0, st, QV_ARGS);
+      break;
+    case QV_EPI_QKROPE:
+      if constexpr (!BF16) hipLaunchKernelGGL((w4a16_ksplit_kernel<BF16, MT, QV_EPI_QKROPE>), grid, block, 0, st, QV_ARGS);
+      break;
+    default:
+      hipLaunchKernelGGL((w4a16_ksplit_kernel<BF16, MT, QV_EPI_BIAS_RESID>), grid, block, 0, st, QV_ARGS);
+      break;
+  }
+#undef QV_ARGS
+}
+
 template <bool BF16, int MT, int MT2 = 0>
 static void launch_mt(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                       const void* gamma, void* out, int M, int N, int K, int epi, hipStream_t st,
@@ -479,7 +590,13 @@ int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void
                         const void* gamma, void* out, int M, int N, int K, int epi, const StreamPlan& p,
                         hipStream_t st, const QkRopeArgs* qk) {
   const QkRopeArgs a = qk ? *qk : QkRopeArgs();
-  if (p.mt_b) {
+  if (p.ksplit) {
+    QV_CHECK_ARG(p.mt_b == 0 && K % 256 == 0, "bad tile plan: K split of K=%d", K);
+    if (p.mt_a == 4) launch_ksplit<BF16, 4>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+    else if (p.mt_a == 3) launch_ksplit<BF16, 3>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+    else if (p.mt_a == 2) launch_ksplit<BF16, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+    else launch_ksplit<BF16, 1>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+  } else if (p.mt_b) {
     QV_CHECK_ARG(p.rows_a > 0 && p.rows_a < M && p.rows_a % (32 * p.mt_a) == 0,
                  "bad tile plan: %d rows of %d-row tiles for M=%d", p.rows_a, 32 * p.mt_a, M);
     if (p.mt_a == 4 && p.mt_b == 3) launch_mt<BF16, 4, 3>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a, p.rows_a);

@@ -556,7 +556,19 @@ def test_two_range_launch_matches_row_slices(gpu, M, N, K, epi_name, dt):
     parts = torch.cat([E.w4a16_linear(x[:cut], qw, scales, zeros, bias=b, epilogue=epi),
                        E.w4a16_linear(x[cut:], qw, scales, zeros, bias=b, epilogue=epi)])
     torch.cuda.synchronize()
-    assert torch.equal(whole, parts)
+    plans = [E.w4a16_plan(m, N, K, epi) for m in (M, cut, M - cut)]
+    assert plans[0]["kernel"] == "stream" and plans[0]["tile2"] > 0, plans[0]
+    if all(pl["kernel"] == "stream" for pl in plans):
+        assert torch.equal(whole, parts)
+    else:
+        # a slice small enough for one tile per CU sums K in two halves: the
+        # fp32 sums differ in rounding only -- one 16-bit step of the value,
+        # plus the fp32 accumulation error (a few 2^-24 of the row's partial
+        # sums), which spans many steps only where the sum cancels to ~0
+        w, pt = whole.float(), parts.float()
+        step = torch.maximum(w.abs(), pt.abs()) * (2.0 ** -7 if dt == "bf16" else 2.0 ** -10)
+        slack = 2.0 ** -20 * w.abs().max().item()
+        assert ((w - pt).abs() <= step + slack).all(), (w - pt).abs().max().item()
     rows = np.random.default_rng(1).choice(M, 256, replace=False)
     xr = x[torch.from_numpy(rows).to(gpu)].float().cpu().numpy()
     if dt == "bf16":
@@ -568,3 +580,61 @@ def test_two_range_launch_matches_row_slices(gpu, M, N, K, epi_name, dt):
         ref = 0.5 * ref * (1.0 + erf(ref / np.sqrt(2.0)))
     got = whole[torch.from_numpy(rows).to(gpu)].float().cpu().numpy()
     assert np.isfinite(got).all() and O.rel_err(got, ref) <= TOL
+
+
+# Launches of at most one tile per CU split K between two wave groups of one
+# workgroup (one case per tile height, with the epilogues the model uses).
+@pytest.mark.parametrize("M,N,K,epi_name,tile", [(1374, 1024, 4096, "BIAS", 32), (1374, 512, 1024, "NONE", 32),
+                                                 (2748, 1024, 4096, "BIAS", 64), (2000, 2048, 2048, "BIAS_GELU", 64),
+                                                 (4000, 2048, 2048, "BIAS", 128), (300, 256, 256, "GELU", 32),
+                                                 (2500, 2048, 2048, "BIAS", 96)])
+def test_ksplit_launch_matches_oracle(gpu, M, N, K, epi_name, tile):
+    """The K-split launch (plan checked) against the fp32 dequantised
+    reference: every row within the tolerance, a re-run bitwise identical."""
+    from scipy.special import erf
+    from qvggt_amd import awq_inference_engine as E
+    from qvggt_amd import _lib
+    epi = getattr(_lib, "QV_EPI_" + epi_name)
+    plan = E.w4a16_plan(M, N, K, epi)
+    assert plan["kernel"] == "stream_ksplit" and plan["tile"] == tile, plan
+    p = O.make_w4_problem(M, K, N, seed=M + 3 * N + K)
+    t = _to_dev(p, gpu)
+    bias = (np.random.default_rng(N).standard_normal(N) * 0.1).astype(np.float16)
+    b = torch.from_numpy(bias).to(gpu)
+    y = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=b, epilogue=epi)
+    y2 = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=b, epilogue=epi)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    W = O.dequantize(p["qweight"], p["scales"], p["scaled_zeros"], N, K)
+    ref = O.gemm_ref(p["x"], W).astype(np.float64)
+    if epi_name in ("BIAS", "BIAS_GELU"):
+        ref = ref + bias.astype(np.float64)
+    if epi_name in ("BIAS_GELU", "GELU"):
+        ref = 0.5 * ref * (1.0 + erf(ref / np.sqrt(2.0)))
+    got = y.float().cpu().numpy()
+    err = O.rel_err(got, ref)
+    print(f"[ksplit] M={M} N={N} K={K} {epi_name} tile {tile}: rel err {err:.3e}", flush=True)
+    assert np.isfinite(got).all() and err <= TOL, err
+
+
+def test_ksplit_residual_matches_unfused(gpu):
+    """The residual epilogue on a K-split launch (M = 1374, one frame's proj)
+    against the same op chain run unfused: the plain linear (also K-split)
+    followed by torch's residual update, within 2 fp16 steps."""
+    from qvggt_amd import awq_inference_engine as E
+    M, K = 1374, 1024
+    assert E.w4a16_plan(M, 1024, K, 1)["kernel"] == "stream_ksplit"
+    rng = np.random.default_rng(11)
+    # residual: r + ls * linear(x)
+    p = O.make_w4_problem(M, K, 1024, seed=5)
+    t = _to_dev(p, gpu)
+    b = torch.from_numpy((rng.standard_normal(1024) * 0.1).astype(np.float16)).to(gpu)
+    gam = torch.from_numpy((rng.standard_normal(1024) * 0.5).astype(np.float16)).to(gpu)
+    r0 = torch.from_numpy(rng.standard_normal((M, 1024)).astype(np.float16)).to(gpu)
+    r = r0.clone()
+    E.w4a16_linear_residual(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], b, gam, r)
+    lin = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=b, epilogue=1)
+    want = r0.clone().addcmul_(lin, gam)
+    torch.cuda.synchronize()
+    step = want.float().abs() * 2.0 ** -10
+    assert ((r.float() - want.float()).abs() <= 2 * step + 1e-7).all()
