@@ -63,9 +63,10 @@ int qv_w4a16_gemm(const void* x, const void* qweight, const void* scales,
  * The launch plan qv_w4a16_gemm (and its residual / q/k-RoPE variants, which
  * plan the same way) picks for an M x K -> N linear, written to plan[4]:
  * plan[0] = 0 skinny kernel (M <= 64), 1 streamed tiles, 2 streamed tiles
- * with K split between two wave groups of one workgroup (launches of at most
- * one tile per CU); plan[1] = tile height of rows [0, plan[2]); plan[3] =
- * tile height of the remaining rows (0: one range).  No device work.  The
+ * with K split between two wave groups of one workgroup, 3 streamed tiles
+ * with 128-k pipeline stages (2 and 3: launches of at most one tile per CU);
+ * plan[1] = tile height of rows [0, plan[2]); plan[3] = tile height of the
+ * remaining rows (0: one range).  No device work.  The
  * reference has no counterpart (its gemm_cuda.cu:1125-1235 picks kernels by
  * M bucket internally); it is here for tests and profiling, which need to
  * know which summation order a launch uses.

@@ -242,13 +242,14 @@ def w4a16_linear_residual(x: torch.Tensor, qweight: torch.Tensor, scales: torch.
 
 def w4a16_plan(M: int, N: int, K: int, epilogue: int = _lib.QV_EPI_NONE) -> dict:
     """The launch plan of an M x K -> N W4A16 linear (no device work):
-    ``kernel`` "skinny", "stream" or "stream_ksplit" (K summed in two halves
-    by two wave groups of one workgroup), ``tile`` rows of the first range,
+    ``kernel`` "skinny", "stream", "stream_ksplit" (K summed in two halves
+    by two wave groups of one workgroup) or "stream_k128" (128-k pipeline
+    stages; same sums as "stream"), ``tile`` rows of the first range,
     ``rows`` the rows it covers, ``tile2`` the second range's tile height
     (0: one range)."""
     plan = (C.c_int32 * 4)()
     _lib.call("qv_w4a16_plan", int(M), int(N), int(K), int(epilogue), C.cast(plan, C.c_void_p))
-    kind = {0: "skinny", 1: "stream", 2: "stream_ksplit"}[plan[0]]
+    kind = {0: "skinny", 1: "stream", 2: "stream_ksplit", 3: "stream_k128"}[plan[0]]
     return {"kernel": kind, "tile": plan[1], "rows": plan[2], "tile2": plan[3]}
 
 

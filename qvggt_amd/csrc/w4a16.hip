@@ -539,6 +539,12 @@ StreamPlan w4_plan_for(int tile, int M, int N, int K, int epi) {
   // measured 2-4 % slower (config 1: 14.67 -> 14.98 us).
   const long tiles = (long)((M + 32 * p.mt_a - 1) / (32 * p.mt_a)) * ((N + 255) / 256);
   p.ksplit = QV_W4_KSPLIT && p.mt_b == 0 && tiles <= 256 && K % 256 == 0 && (K >= 2048 || p.mt_a == 1);
+  // The other one-round launches of 64- and 96-row tiles pipeline 128-k
+  // stages: a stage's loads get twice the time to land behind one wave's
+  // MFMAs, and half as many barriers (config 1, 1374 x 1024 -> 3072:
+  // 15.0 -> 14.5 us; 1000 x 1024 -> 3072 -3 %; bit-identical).  With two
+  // workgroups per CU the shorter stages measured equal or faster.
+  p.sub = (p.mt_b == 0 && !p.ksplit && tiles <= 256 && K % 256 == 0 && (p.mt_a == 2 || p.mt_a == 3)) ? 2 : 1;
   return p;
 }
 }  // namespace
@@ -950,7 +956,7 @@ extern "C" int qv_w4a16_plan(int64_t M, int64_t N, int64_t K, int epilogue, int3
     return QV_OK;
   }
   const StreamPlan p = w4_plan_for(tile, (int)M, (int)N, (int)K, epilogue);
-  plan[0] = p.ksplit ? 2 : 1;
+  plan[0] = p.ksplit ? 2 : (p.sub == 2 ? 3 : 1);
   plan[1] = 32 * p.mt_a;
   plan[2] = p.mt_b ? p.rows_a : (int32_t)M;
   plan[3] = 32 * p.mt_b;

@@ -152,6 +152,7 @@ __device__ __forceinline__ void epilogue_apply4v(const uint2& b, float (&r)[4]) 
 struct StreamPlan {
   int mt_a = 4, rows_a = 0, mt_b = 0;
   bool ksplit = false;   // one range of mt_a tiles, K split between two 4-wave groups
+  int sub = 1;           // 64-k sub-stages per pipeline stage (2: one range of 64- or 96-row tiles, K % 256 == 0)
 };
 
 // Streamed (LDS-pipelined, 32x32 MFMA) GEMM, tiles (32 mt) x 256.

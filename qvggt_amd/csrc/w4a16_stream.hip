@@ -36,7 +36,7 @@ constexpr int EP = 128;  // bytes per staged epilogue row (64 fp16, chunk-swizzl
 
 // Main loop of one tile over its 64-k stages [k0, k1): acc += the tile's
 // products (acc is not cleared here).  Returns with every load landed.
-template <bool BF16, int MT>
+template <bool BF16, int MT, int SUB = 1>
 __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const uint16_t* __restrict__ x,
                                                 const uint32_t* __restrict__ qw,
                                                 const uint16_t* __restrict__ scales,
@@ -44,11 +44,11 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
                                                 int n0, int k0, int k1, f32x16 (&acc)[2][MT]) {
   constexpr int BM = 32 * MT, NT = 2;
   constexpr int A_BYTES = BM * 128;
-  constexpr int STAGE = A_BYTES;
+  constexpr int STAGE = SUB * A_BYTES;
   constexpr int NSTAGE = 3;
   constexpr int A_INSTR = BM / 32;                // 1 KB direct loads per wave for A
-  static_assert(A_INSTR < 16, "vmcnt immediate");
-  static_assert(NSTAGE * STAGE <= 4 * BM * EP, "the epilogue staging is the larger LDS user");
+  static_assert(SUB * A_INSTR < 16, "vmcnt immediate");
+  static_assert(SUB == 1 || SUB == 2, "64- or 128-k stages");
 
   // threadIdx.x through an empty asm: the lane-dependent addresses below are
   // then computed here, not hoisted out of a caller's loop over tiles and
@@ -86,22 +86,27 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
     b_voff[j] = (uint32_t)((n >> 2) * K2 + 32 * (n & 3) + 16 * h);
     sz_voff[j] = (uint32_t)(n * 2);
   }
-  auto load_b = [&](int ks, uint4 (&wq)[NT], uint32_t (&sv)[NT], uint32_t (&zv)[NT]) {
+  auto load_b = [&](int ks, uint4 (&wq)[SUB][NT], uint32_t (&sv)[NT], uint32_t (&zv)[NT]) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      wq[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsB, b_voff[j], ks * 128, 0));
-      sv[j] = __builtin_amdgcn_raw_buffer_load_b16(rsS, sz_voff[j], (ks >> 1) * N * 2, 0);
-      zv[j] = __builtin_amdgcn_raw_buffer_load_b16(rsZ, sz_voff[j], (ks >> 1) * N * 2, 0);
+#pragma unroll
+      for (int u = 0; u < SUB; ++u)
+        wq[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsB, b_voff[j], (SUB * ks + u) * 128, 0));
+      sv[j] = __builtin_amdgcn_raw_buffer_load_b16(rsS, sz_voff[j], ((SUB * ks) >> 1) * N * 2, 0);
+      zv[j] = __builtin_amdgcn_raw_buffer_load_b16(rsZ, sz_voff[j], ((SUB * ks) >> 1) * N * 2, 0);
     }
   };
 
   const uint32_t lds0 = lds_addr(lds);
   auto issue = [&](int ks, int st) {
-    const uint32_t base = lds0 + st * STAGE;
 #pragma unroll
-    for (int q = 0; q < A_INSTR; ++q) {
-      const int r0 = 8 * (A_INSTR * wave + q);
-      lds_dma16(rsA, a_voff[(r0 >> 3) & 1], r0 * K2 + ks * 128, base + r0 * 128);
+    for (int u = 0; u < SUB; ++u) {
+      const uint32_t base = lds0 + st * STAGE + u * A_BYTES;
+#pragma unroll
+      for (int q = 0; q < A_INSTR; ++q) {
+        const int r0 = 8 * (A_INSTR * wave + q);
+        lds_dma16(rsA, a_voff[(r0 >> 3) & 1], r0 * K2 + (SUB * ks + u) * 128, base + r0 * 128);
+      }
     }
   };
 
@@ -118,9 +123,9 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
       }
     }
   };
-  // activation fragments of k-step s of the stage in LDS buffer st
-  auto read_a = [&](int st, int s, uint4 (&af)[MT]) {
-    const uint8_t* base = lds + st * STAGE;
+  // activation fragments of k-step s of 64-k half u of the stage in LDS buffer st
+  auto read_a = [&](int st, int u, int s, uint4 (&af)[MT]) {
+    const uint8_t* base = lds + st * STAGE + u * A_BYTES;
     const uint32_t col = (uint32_t)(((4 * h + s) ^ fa) * 16);
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[i] = *reinterpret_cast<const uint4*>(base + (32 * i + l32) * 128 + col);
@@ -133,30 +138,31 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   // stage's first MFMAs do not wait behind its barrier for LDS reads and a
   // dequantisation; af0 / wf0 hold those fragments on exit.  The scheduling
   // fences keep the compiler from sinking the reads next to their use.
-  auto compute = [&](int st, int nst, const uint4 (&wq)[NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT],
-                     const uint4 (&nwq)[NT], const uint32_t (&nsv)[NT], const uint32_t (&nzv)[NT], uint4 (&af0)[MT],
+  auto compute = [&](int st, int nst, const uint4 (&wq)[SUB][NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT],
+                     const uint4 (&nwq)[SUB][NT], const uint32_t (&nsv)[NT], const uint32_t (&nzv)[NT], uint4 (&af0)[MT],
                      uint4 (&wf0)[NT]) {
+    constexpr int T = 4 * SUB;   // k-steps per stage
     uint4 af[2][MT], wf[2][NT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[0][i] = af0[i];
 #pragma unroll
     for (int j = 0; j < NT; ++j) wf[0][j] = wf0[j];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s < 3) read_a(st, s + 1, af[(s + 1) & 1]);
-      else read_a(nst, 0, af[0]);
+    for (int t = 0; t < T; ++t) {
+      if (t < T - 1) read_a(st, (t + 1) >> 2, (t + 1) & 3, af[(t + 1) & 1]);
+      else read_a(nst, 0, 0, af[0]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) acc[j][i] = mfma32<BF16>(wf[s & 1][j], af[s & 1][i], acc[j][i]);
+        for (int j = 0; j < NT; ++j) acc[j][i] = mfma32<BF16>(wf[t & 1][j], af[t & 1][i], acc[j][i]);
       }
-      if (s < 3) {
-        dq(s + 1, wq, sv, zv, wf[(s + 1) & 1]);
+      if (t < T - 1) {
+        dq((t + 1) & 3, wq[(t + 1) >> 2], sv, zv, wf[(t + 1) & 1]);
       } else {
         // the next stage's weights (and every copy issued before them) have landed
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-        dq(0, nwq, nsv, nzv, wf[0]);
+        dq(0, nwq[0], nsv, nzv, wf[0]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -181,26 +187,28 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   // a dead register set), so every stage issues the same count.  (An odd
   // stage count, with a conditional second half, made the compiler spill the
   // accumulators in a kernel that loops over tiles.)
-  uint4 wq0[NT], wq1[NT];
+  uint4 wq0[SUB][NT], wq1[SUB][NT];
   uint32_t sv0[NT], zv0[NT], sv1[NT], zv1[NT];
   uint4 af0[MT], wf0[NT];
-  const int last = k1 - 1, nks = k1 - k0;
-  issue(k0, 0);
-  issue(k0 + 1 < k1 ? k0 + 1 : last, 1);
-  load_b(k0, wq0, sv0, zv0);
+  // stage indices in units of SUB x 64 k
+  const int L0 = k0 / SUB, L1 = k1 / SUB;
+  const int last = L1 - 1, nks = L1 - L0;
+  issue(L0, 0);
+  issue(L0 + 1 < L1 ? L0 + 1 : last, 1);
+  load_b(L0, wq0, sv0, zv0);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): A(k0), A(k0 + 1), B(k0)
   lds_barrier();
-  read_a(0, 0, af0);
-  dq(0, wq0, sv0, zv0, wf0);
+  read_a(0, 0, 0, af0);
+  dq(0, wq0[0], sv0, zv0, wf0);
   for (int i = 0; i < nks; i += 2) {
-    const int ks = k0 + i;
+    const int ks = L0 + i;
     lds_barrier();
-    issue(ks + 2 < k1 ? ks + 2 : last, (i + 2) % NSTAGE);
+    issue(ks + 2 < L1 ? ks + 2 : last, (i + 2) % NSTAGE);
     load_b(ks + 1, wq1, sv1, zv1);
     compute(i % NSTAGE, (i + 1) % NSTAGE, wq0, sv0, zv0, wq1, sv1, zv1, af0, wf0);
     lds_barrier();
-    issue(ks + 3 < k1 ? ks + 3 : last, (i + 3) % NSTAGE);
-    load_b(ks + 2 < k1 ? ks + 2 : last, wq0, sv0, zv0);
+    issue(ks + 3 < L1 ? ks + 3 : last, (i + 3) % NSTAGE);
+    load_b(ks + 2 < L1 ? ks + 2 : last, wq0, sv0, zv0);
     compute((i + 1) % NSTAGE, (i + 2) % NSTAGE, wq1, sv1, zv1, wq0, sv0, zv0, af0, wf0);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the repeated loads may not land during the epilogue
@@ -399,7 +407,7 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
 }
 
 // One whole tile: logical tile lid of the rows from m_base.
-template <bool BF16, int MT, int EPI>
+template <bool BF16, int MT, int EPI, int SUB = 1>
 __device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uint16_t* __restrict__ x,
                                             const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scales,
                                             const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
@@ -414,7 +422,7 @@ __device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uin
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
-  stream_mainloop<BF16, MT>(lds, x, qw, scales, zeros, M, N, K, m0, n0, 0, K >> 6, acc);
+  stream_mainloop<BF16, MT, SUB>(lds, x, qw, scales, zeros, M, N, K, m0, n0, 0, K >> 6, acc);
   stream_epilogue<BF16, MT, EPI>(lds, bias, gamma, out, M, N, qk, m0, n0, acc);
 }
 
@@ -422,7 +430,7 @@ __device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uin
 // rows [0, m_split), the rest 32*MT2-row tiles of rows [m_split, M) (MT2 = 0:
 // one range).  Each range maps its blocks to tiles on its own (xcd_remap of
 // the block's index within the range).
-template <bool BF16, int MT, int MT2, int EPI>
+template <bool BF16, int MT, int MT2, int EPI, int SUB = 1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
                            const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -430,10 +438,11 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
                            uint16_t* __restrict__ out, int M, int N, int K, int tiles_n, QkRopeArgs qk,
                            int n_first, int m_split) {
   constexpr int MTX = MT > MT2 ? MT : MT2;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * 32 * MTX * 128];
+  constexpr int LDS_B = (SUB == 2 ? 6 : 4) * 32 * MTX * 128;   // max(3 stages, the epilogue staging)
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_B];
   const int b = blockIdx.x;
   if (MT2 == 0 || b < n_first) {
-    stream_tile<BF16, MT, EPI>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
+    stream_tile<BF16, MT, EPI, SUB>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
                                xcd_remap(b, MT2 == 0 ? (int)gridDim.x : n_first), 0);
   } else {
     stream_tile<BF16, (MT2 > 0 ? MT2 : 1), EPI>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
@@ -550,7 +559,7 @@ static void launch_ksplit(const void* x, const void* qw, const void* s, const vo
 #undef QV_ARGS
 }
 
-template <bool BF16, int MT, int MT2 = 0>
+template <bool BF16, int MT, int MT2 = 0, int SUB = 1>
 static void launch_mt(const void* x, const void* qw, const void* s, const void* z, const void* bias,
                       const void* gamma, void* out, int M, int N, int K, int epi, hipStream_t st,
                       const QkRopeArgs& qk, int m_split = 0) {
@@ -564,22 +573,22 @@ static void launch_mt(const void* x, const void* qw, const void* s, const void* 
       (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, tiles_n, qk, n_first, m_split
   switch (epi) {
     case QV_EPI_NONE:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_NONE>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_NONE, SUB>), grid, block, 0, st, QV_ARGS);
       break;
     case QV_EPI_BIAS:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS, SUB>), grid, block, 0, st, QV_ARGS);
       break;
     case QV_EPI_BIAS_GELU:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS_GELU>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS_GELU, SUB>), grid, block, 0, st, QV_ARGS);
       break;
     case QV_EPI_GELU:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_GELU>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_GELU, SUB>), grid, block, 0, st, QV_ARGS);
       break;
     case QV_EPI_QKROPE:
-      if constexpr (!BF16) hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_QKROPE>), grid, block, 0, st, QV_ARGS);
+      if constexpr (!BF16) hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_QKROPE, SUB>), grid, block, 0, st, QV_ARGS);
       break;
     default:
-      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS_RESID>), grid, block, 0, st, QV_ARGS);
+      hipLaunchKernelGGL((w4a16_stream32_kernel<BF16, MT, MT2, QV_EPI_BIAS_RESID, SUB>), grid, block, 0, st, QV_ARGS);
       break;
   }
 #undef QV_ARGS
@@ -603,6 +612,12 @@ int launch_w4a16_stream(const void* x, const void* qw, const void* s, const void
     else if (p.mt_a == 4 && p.mt_b == 2) launch_mt<BF16, 4, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a, p.rows_a);
     else if (p.mt_a == 3 && p.mt_b == 2) launch_mt<BF16, 3, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a, p.rows_a);
     else QV_CHECK_ARG(false, "bad tile plan: tile pair %d/%d", p.mt_a, p.mt_b);
+  } else if (p.sub == 2) {
+    QV_CHECK_ARG(K % 256 == 0 && (p.mt_a == 2 || p.mt_a == 3),
+                 "bad tile plan: 128-k stages need K %% 256 == 0 and 64- or 96-row tiles (K=%d, tile %d)", K,
+                 32 * p.mt_a);
+    if (p.mt_a == 3) launch_mt<BF16, 3, 0, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
+    else launch_mt<BF16, 2, 0, 2>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
   } else if (p.mt_a == 4) {
     launch_mt<BF16, 4>(x, qw, s, z, bias, gamma, out, M, N, K, epi, st, a);
   } else if (p.mt_a == 3) {

@@ -558,7 +558,7 @@ def test_two_range_launch_matches_row_slices(gpu, M, N, K, epi_name, dt):
     torch.cuda.synchronize()
     plans = [E.w4a16_plan(m, N, K, epi) for m in (M, cut, M - cut)]
     assert plans[0]["kernel"] == "stream" and plans[0]["tile2"] > 0, plans[0]
-    if all(pl["kernel"] == "stream" for pl in plans):
+    if all(pl["kernel"] in ("stream", "stream_k128") for pl in plans):
         assert torch.equal(whole, parts)
     else:
         # a slice small enough for one tile per CU sums K in two halves: the
@@ -582,21 +582,26 @@ def test_two_range_launch_matches_row_slices(gpu, M, N, K, epi_name, dt):
     assert np.isfinite(got).all() and O.rel_err(got, ref) <= TOL
 
 
-# Launches of at most one tile per CU split K between two wave groups of one
-# workgroup (one case per tile height, with the epilogues the model uses).
-@pytest.mark.parametrize("M,N,K,epi_name,tile", [(1374, 1024, 4096, "BIAS", 32), (1374, 512, 1024, "NONE", 32),
-                                                 (2748, 1024, 4096, "BIAS", 64), (2000, 2048, 2048, "BIAS_GELU", 64),
-                                                 (4000, 2048, 2048, "BIAS", 128), (300, 256, 256, "GELU", 32),
-                                                 (2500, 2048, 2048, "BIAS", 96)])
-def test_ksplit_launch_matches_oracle(gpu, M, N, K, epi_name, tile):
-    """The K-split launch (plan checked) against the fp32 dequantised
+# Launches of at most one tile per CU: K split between two wave groups of one
+# workgroup, or 128-k pipeline stages (one case per tile height, with the
+# epilogues the model uses).
+@pytest.mark.parametrize("M,N,K,epi_name,tile,kind", [
+    (1374, 1024, 4096, "BIAS", 32, "stream_ksplit"), (1374, 512, 1024, "NONE", 32, "stream_ksplit"),
+    (2748, 1024, 4096, "BIAS", 64, "stream_ksplit"), (2000, 2048, 2048, "BIAS_GELU", 64, "stream_ksplit"),
+    (4000, 2048, 2048, "BIAS", 128, "stream_ksplit"), (300, 256, 256, "GELU", 32, "stream_ksplit"),
+    (2500, 2048, 2048, "BIAS", 96, "stream_ksplit"),
+    (1374, 3072, 1024, "BIAS", 96, "stream_k128"), (1000, 3072, 1024, "NONE", 64, "stream_k128"),
+    (1374, 4096, 1024, "BIAS_GELU", 96, "stream_k128"), (2000, 3072, 256, "GELU", 96, "stream_k128"),
+    (1500, 2048, 512, "BIAS", 64, "stream_k128")])
+def test_one_round_launch_matches_oracle(gpu, M, N, K, epi_name, tile, kind):
+    """The one-round launch (plan checked) against the fp32 dequantised
     reference: every row within the tolerance, a re-run bitwise identical."""
     from scipy.special import erf
     from qvggt_amd import awq_inference_engine as E
     from qvggt_amd import _lib
     epi = getattr(_lib, "QV_EPI_" + epi_name)
     plan = E.w4a16_plan(M, N, K, epi)
-    assert plan["kernel"] == "stream_ksplit" and plan["tile"] == tile, plan
+    assert plan["kernel"] == kind and plan["tile"] == tile, plan
     p = O.make_w4_problem(M, K, N, seed=M + 3 * N + K)
     t = _to_dev(p, gpu)
     bias = (np.random.default_rng(N).standard_normal(N) * 0.1).astype(np.float16)
@@ -613,7 +618,7 @@ def test_ksplit_launch_matches_oracle(gpu, M, N, K, epi_name, tile):
         ref = 0.5 * ref * (1.0 + erf(ref / np.sqrt(2.0)))
     got = y.float().cpu().numpy()
     err = O.rel_err(got, ref)
-    print(f"[ksplit] M={M} N={N} K={K} {epi_name} tile {tile}: rel err {err:.3e}", flush=True)
+    print(f"[{kind}] M={M} N={N} K={K} {epi_name} tile {tile}: rel err {err:.3e}", flush=True)
     assert np.isfinite(got).all() and err <= TOL, err
 
 
@@ -631,6 +636,41 @@ def test_ksplit_residual_matches_unfused(gpu):
     b = torch.from_numpy((rng.standard_normal(1024) * 0.1).astype(np.float16)).to(gpu)
     gam = torch.from_numpy((rng.standard_normal(1024) * 0.5).astype(np.float16)).to(gpu)
     r0 = torch.from_numpy(rng.standard_normal((M, 1024)).astype(np.float16)).to(gpu)
+    r = r0.clone()
+    E.w4a16_linear_residual(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], b, gam, r)
+    lin = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=b, epilogue=1)
+    want = r0.clone().addcmul_(lin, gam)
+    torch.cuda.synchronize()
+    step = want.float().abs() * 2.0 ** -10
+    assert ((r.float() - want.float()).abs() <= 2 * step + 1e-7).all()
+
+
+def test_k128_bf16_and_residual(gpu):
+    """128-k stages with bf16 operands (1000 x 1024 -> 3072) against the bf16
+    dequantised reference, and the residual epilogue on a 128-k launch
+    (5496 x 1024 -> 1024) against the unfused chain, within 2 16-bit steps."""
+    from qvggt_amd import awq_inference_engine as E
+    M, N, K = 1000, 3072, 1024
+    assert E.w4a16_plan(M, N, K, 0)["kernel"] == "stream_k128"
+    p = O.make_w4_problem(M, K, N, seed=77)
+    xb, sc, sz = _bf16_problem(p)
+    x = torch.from_numpy(xb.view(np.int16)).to(gpu).view(torch.bfloat16).view(M, K)
+    qw = torch.from_numpy(p["qweight"]).to(gpu)
+    sct = torch.from_numpy(sc.view(np.int16)).to(gpu).view(torch.bfloat16)
+    szt = torch.from_numpy(sz.view(np.int16)).to(gpu).view(torch.bfloat16)
+    y = E.gemm_forward_cuda_new(x, qw, sct, szt)
+    W = O.bf16_bits_to_f32(O.dequantize_bf16_bits(p["qweight"], sc, sz, N, K))
+    ref = O.bf16_bits_to_f32(xb) @ W.T
+    err = O.rel_err(y.float().cpu().numpy(), ref)
+    assert err <= TOL, err
+    M, N = 5496, 1024
+    assert E.w4a16_plan(M, N, K, 1)["kernel"] == "stream_k128"
+    rng = np.random.default_rng(3)
+    p = O.make_w4_problem(M, K, N, seed=6)
+    t = _to_dev(p, gpu)
+    b = torch.from_numpy((rng.standard_normal(N) * 0.1).astype(np.float16)).to(gpu)
+    gam = torch.from_numpy((rng.standard_normal(N) * 0.5).astype(np.float16)).to(gpu)
+    r0 = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float16)).to(gpu)
     r = r0.clone()
     E.w4a16_linear_residual(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], b, gam, r)
     lin = E.w4a16_linear(t["x"], t["qweight"], t["scales"], t["scaled_zeros"], bias=b, epilogue=1)
