@@ -28,7 +28,9 @@
 //    registers 8p..8p+7 of block kb, i.e. keys 32kb + 16p + {0..3, 8..11} + 4h.
 //  * K and V tiles arrive by LDS DMA in their natural [key][dim] layout
 //    (128-byte rows; 16-byte chunk c of row r at c ^ fk(r) for K and
-//    c ^ fv(r) for V), one tile ahead.
+//    c ^ fv(r) for V), one DMA tile of 128 keys ahead; each DMA tile is
+//    consumed as two 64-key compute tiles, so the workgroup meets at one
+//    barrier per 128 keys (1-2 % faster than one per 64, bit-identical).
 //  * V^T (the PV A operand) comes out of LDS through ds_read_b64_tr_b16: two
 //    transposed 8-byte reads give each lane its dim's 8 keys in k-slot order,
 //    with no register staging or transposed stores.
@@ -39,8 +41,10 @@ namespace qv {
 constexpr int ATT_QW = 64;                 // queries per wave (two 32-query blocks)
 constexpr int ATT_WAVES = 4;               // waves per workgroup
 constexpr int ATT_BQ = ATT_WAVES * ATT_QW; // queries per workgroup
-constexpr int ATT_DMA = 8 / ATT_WAVES;     // 1 KB (8-key) DMA rows per wave per tile, K and V each
-constexpr int ATT_BK = 64;                 // keys per tile
+constexpr int ATT_BK = 64;                 // keys per compute tile
+constexpr int ATT_SUB = 2;                 // compute tiles per DMA tile (one barrier per DMA tile)
+constexpr int ATT_BKD = ATT_BK * ATT_SUB;  // keys per DMA tile
+constexpr int ATT_DMA = ATT_BKD / 8 / ATT_WAVES;  // 1 KB (8-key) DMA rows per wave per DMA tile, K and V each
 
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units: P <= 256 between rescales
 constexpr float P_SUM_LIMIT = 256.0f;  // 2^RESCALE_SLACK: a lane's tile sum above it may hide a P above it
@@ -87,8 +91,8 @@ __device__ __forceinline__ float half_sum(float x) {
 __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ out, int L, int H, long q_ts, long kv_ts, long v_ts, long o_ts, float scale_log2) {
-  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][ATT_BK * 128];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[2][ATT_BK * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][ATT_BKD * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[2][ATT_BKD * 128];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
     }
   }
 
-  // ---- K tile DMA: 8 x 1 KB per tile, 2 per wave; lane L lands at key
+  // ---- K tile DMA: 16 x 1 KB per DMA tile, 4 per wave; lane L lands at key
   // r0 + L/8, physical chunk L%8, so it fetches logical chunk (L%8) ^ fk(row).
   const auto rsK = make_rsrc(k + tok0 * kv_ts + (long)head * 64, (uint64_t)L * kv_ts * 2);
   uint32_t k_voff[ATT_DMA];
@@ -144,8 +148,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int w2 = 0; w2 < ATT_DMA; ++w2) {
       const int r0 = 8 * (ATT_DMA * wave + w2);
-      lds_dma16(rsK, k_voff[w2], (uint32_t)((tile * ATT_BK + r0) * kv_ts * 2),
-                klds0 + buf * (ATT_BK * 128) + r0 * 128);
+      lds_dma16(rsK, k_voff[w2], (uint32_t)((tile * ATT_BKD + r0) * kv_ts * 2),
+                klds0 + buf * (ATT_BKD * 128) + r0 * 128);
     }
   };
   // ---- V tile DMA, natural [key][dim] layout with the fv swizzle
@@ -162,8 +166,8 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int w2 = 0; w2 < ATT_DMA; ++w2) {
       const int r0 = 8 * (ATT_DMA * wave + w2);
-      lds_dma16(rsV, v_voff[w2], (uint32_t)((tile * ATT_BK + r0) * v_ts * 2),
-                vlds0 + buf * (ATT_BK * 128) + r0 * 128);
+      lds_dma16(rsV, v_voff[w2], (uint32_t)((tile * ATT_BKD + r0) * v_ts * 2),
+                vlds0 + buf * (ATT_BKD * 128) + r0 * 128);
     }
   };
   // Transposed V^T fragments: for k-step st (keys 16 st + {0..3, 8..11} + 4h
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
   // for reads r = 0, 1; the transpose hands lane l32 its dim's 8 keys.
   const int tr_key = 4 * h + ((lane & 15) >> 2);
   const int tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const int ntiles = (L + ATT_BK - 1) / ATT_BK;
+  const int ntiles = (L + ATT_BKD - 1) / ATT_BKD;   // DMA tiles
   f32x16 o[2][2];   // [query block][dim block]
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
@@ -190,18 +194,10 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
   float base[2] = {0.f, 0.f};
   const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-  auto tile = [&](int j, bool mask) {
-    const int buf = j & 1;
-    const bool more = j + 1 < ntiles;
-    if (more) {
-      issue_k(j + 1, buf ^ 1);
-      issue_v(j + 1, buf ^ 1);
-    }
-    // a wave whose 64 queries all lie past the sequence end (the last query
-    // tile of a frame) only issues its share of the DMA and keeps the barriers
-    if (live) {
-      // ---- S^T = K Q^T for the 64 keys of tile j, both query blocks (raw dot products)
-      const uint8_t* kb_lds = k_lds[buf];
+  // one 64-key compute tile: keys key0.., K / V rows at kb_lds / vb
+  auto ctile = [&](int key0, const uint8_t* kb_lds, const uint8_t* vb, bool mask) __attribute__((always_inline)) {
+    {
+      // ---- S^T = K Q^T for the 64 keys of the tile, both query blocks (raw dot products)
       f32x16 sc[2][2];   // [query block][key block]
   #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -219,7 +215,6 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
       }
       // ---- V^T fragments of this tile, read before the softmax so their LDS
       // latency hides behind it (the PV MFMAs below consume them)
-      const uint8_t* vb = v_lds[buf];
       uint4 vfr[2][4];
   #pragma unroll
       for (int db = 0; db < 2; ++db) {
@@ -239,12 +234,12 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
   #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         if (mask) {
-          const int key0 = j * ATT_BK + 4 * h;
+          const int kh = key0 + 4 * h;
   #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
   #pragma unroll
             for (int r = 0; r < 16; ++r)
-              if (key0 + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[qb][kb][r] = -INFINITY;
+              if (kh + 32 * kb + 8 * (r >> 2) + (r & 3) >= L) sc[qb][kb][r] = -INFINITY;
         }
         // ---- P = 2^S' = 2^(S - m_use) in fp16 against the current reference,
         // with this tile's partial row sum t (v_dot2 on the fp16 values).  The
@@ -309,6 +304,27 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
                                                               __builtin_bit_cast(f16x8, pf[qb][st]), o[qb][db], 0, 0, 0);
       }
     }
+  };
+  auto tile = [&](int j, bool last) {
+    const int buf = j & 1;
+    const bool more = j + 1 < ntiles;
+    if (more) {
+      issue_k(j + 1, buf ^ 1);
+      issue_v(j + 1, buf ^ 1);
+    }
+    // a wave whose 64 queries all lie past the sequence end (the last query
+    // tile of a frame) only issues its share of the DMA and keeps the barriers
+    if (live) {
+#pragma unroll
+      for (int u = 0; u < ATT_SUB; ++u) {
+        const int key0 = j * ATT_BKD + u * ATT_BK;
+        if (!last) {
+          ctile(key0, k_lds[buf] + u * ATT_BK * 128, v_lds[buf] + u * ATT_BK * 128, false);
+        } else if (key0 < L) {
+          ctile(key0, k_lds[buf] + u * ATT_BK * 128, v_lds[buf] + u * ATT_BK * 128, key0 + ATT_BK > L);
+        }
+      }
+    }
     if (more) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next K and V tiles landed
     lds_barrier();
   };
@@ -317,7 +333,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(
   issue_v(0, 0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   lds_barrier();
-  const int nfull = L / ATT_BK;        // tiles with every key valid
+  const int nfull = L / ATT_BKD;       // DMA tiles with every key valid
   for (int j = 0; j < nfull; ++j) tile(j, false);
   if (nfull < ntiles) tile(nfull, true);
 
