@@ -44,7 +44,7 @@ namespace qv {
 // a workspace overlap.  The last split reads the SK partials back in ks
 // order -- the sum order never depends on arrival order -- and runs the
 // epilogue.  No workgroup waits on another.
-template <bool BF16, int MB, int NB>
+template <bool BF16, int MB, int NB, bool SPLIT>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB == 1 ? 8 : 1))) void w4a16_skinny_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ qw,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ zeros,
@@ -58,8 +58,13 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
   const int nwaves = blockDim.x >> 6;
   const int g = lane >> 4, li = lane & 15;
   const int n0 = blockIdx.x * 16 * NB;
-  const int SK = gridDim.y, ks = blockIdx.y;
-  const int kt_lo = (int)((int64_t)ks * (K >> 7) / SK), kt_hi = (int)((int64_t)(ks + 1) * (K >> 7) / SK);
+  // SPLIT: gridDim.y > 1; the unsplit instance carries no fix-up code
+  const int SK = SPLIT ? (int)gridDim.y : 1, ks = SPLIT ? (int)blockIdx.y : 0;
+  // SK is 1, 2 or 4 (launch_skinny): the k-range bounds by shifts -- a 64-bit
+  // division here expanded to ~300 instructions ahead of the first load, which
+  // cost the unsplit launches 6-19 % (measured against the build without it)
+  const int sk_log = __builtin_ctz((unsigned)SK);
+  const int kt_lo = (ks * (K >> 7)) >> sk_log, kt_hi = ((ks + 1) * (K >> 7)) >> sk_log;
   const uint32_t K2 = (uint32_t)K * 2;
   const auto rsX = make_rsrc(x, (uint64_t)M * K2);
   const uint32_t x_voff = (uint32_t)li * K2 + (uint32_t)g * 64;
@@ -185,13 +190,13 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(MB * NB ==
       float v = 0.f;
       for (int w = 0; w < nwaves; ++w) v += red[w][mb][l][r];
       const int c = 4 * (l >> 4) + r;
-      if (SK == 1)
+      if constexpr (!SPLIT)
         epilogue(v, m, n0 + 16 * j + c);
       else
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), rsP, slot(ks, j, m, c), 0, 16 /*sc1*/);
     }
   }
-  if (SK == 1) return;
+  if constexpr (!SPLIT) return;
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial values are stored
   __syncthreads();
   if (tid == 0)
@@ -638,10 +643,15 @@ static int launch_skinny(const void* x, const void* qw, const void* s, const voi
   int* cnt = sk > 1 ? ws.cnt + (sk == 2 ? 0 : SPLIT_MAX_BLOCKS) : nullptr;
   QV_CHECK_ARG(sk == 1 || ((sk == 2 || sk == 4) && (int)grid.x < SPLIT_MAX_BLOCKS && ws.cnt_n >= 2 * SPLIT_MAX_BLOCKS),
                "w4a16 skinny: bad split plan (%d splits over %d blocks)", sk, (int)grid.x);
-#define QV_SKINNY(MB, NB)                                                                         \
-  hipLaunchKernelGGL((w4a16_skinny_kernel<BF16, MB, NB>), grid, block, 0, st, (const uint16_t*)x, \
-                     (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,                 \
+#define QV_SKINNY_L(MB, NB, SP)                                                                       \
+  hipLaunchKernelGGL((w4a16_skinny_kernel<BF16, MB, NB, SP>), grid, block, 0, st, (const uint16_t*)x, \
+                     (const uint32_t*)qw, (const uint16_t*)s, (const uint16_t*)z,                     \
                      (const uint16_t*)bias, (const uint16_t*)gamma, (uint16_t*)out, M, N, K, epi, part, cnt)
+#define QV_SKINNY(MB, NB)                   \
+  do {                                      \
+    if (sk > 1) QV_SKINNY_L(MB, NB, true);  \
+    else QV_SKINNY_L(MB, NB, false);        \
+  } while (0)
 #define QV_SKINNY_M(NB)            \
   if (M <= 16) QV_SKINNY(1, NB);   \
   else if (M <= 32) QV_SKINNY(2, NB); \
@@ -651,6 +661,7 @@ static int launch_skinny(const void* x, const void* qw, const void* s, const voi
   else { QV_SKINNY_M(1) }
 #undef QV_SKINNY_M
 #undef QV_SKINNY
+#undef QV_SKINNY_L
   return check_launch("w4a16_skinny");
 }
 
