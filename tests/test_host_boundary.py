@@ -200,3 +200,29 @@ def test_tanh_table_lookup_on_every_fp16_pattern():
     nan = m > 0x7C00
     assert np.array_equal(got[~nan], want[~nan])
     assert np.all((got[nan] & 0x7FFF) == 0x3C00)
+
+
+@pytest.mark.parametrize("M,N,K,epi,kind,tile,tile2", [
+    (1, 3072, 1024, 1, "skinny", 0, 0),            # M <= 64: the skinny kernel
+    (64, 1024, 4096, 1, "skinny", 0, 0),
+    (1374, 3072, 1024, 1, "stream_k128", 96, 0),   # config 1: one round, 128-k stages
+    (1000, 3072, 1024, 1, "stream_k128", 64, 0),
+    (1374, 1024, 4096, 1, "stream_ksplit", 32, 0), # one round, K >= 2048: K split in the workgroup
+    (2748, 1024, 4096, 1, "stream_ksplit", 64, 0),
+    (1374, 1024, 1024, 1, "stream_ksplit", 32, 0), # one round of 32-row tiles
+    (10992, 4096, 1024, 2, "stream", 128, 96),     # fc1 of the benchmark: two tile heights
+    (10992, 1024, 4096, 1, "stream", 128, 64),     # fc2: one 128-row tile per CU, then 64-row tiles
+])
+def test_w4a16_plan_rules(M, N, K, epi, kind, tile, tile2):
+    """The launch plan qv_w4a16_gemm picks (host-side planning, no device
+    work): the kernel form per shape and the tile heights."""
+    p = E.w4a16_plan(M, N, K, epi)
+    assert p["kernel"] == kind and p["tile"] == tile and p["tile2"] == tile2, p
+    if kind.startswith("stream"):
+        assert 0 < p["rows"] <= M and (p["tile2"] or p["rows"] == M)
+
+
+def test_w4a16_plan_rejects_bad_shapes():
+    for args in [(0, 64, 128, 0), (8, 64, 100, 0), (8, 60, 128, 0), (8, 64, 128, 9)]:
+        with pytest.raises(RuntimeError):
+            E.w4a16_plan(*args)
