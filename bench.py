@@ -86,7 +86,7 @@ def _median_time(fn, reps: int):
 
 
 def cpu_baseline_mlp(x, w1, b1, w2, b2, y, M_sample: int = 2748, reps: int = 5):
-    """CPU leg (BASELINE.md section 3): the reference's semantics on the host
+    """CPU leg: the reference's semantics on the host
     for fc1 -> GELU -> fc2 on the first M_sample tokens of the benchmark's own
     inputs (two frames), timed as dequantisation alone (the oracle's numpy
     w = q * s + sz of both weight matrices), the fp32 matmuls + erf-GELU alone
@@ -131,7 +131,7 @@ def cpu_baseline_mlp(x, w1, b1, w2, b2, y, M_sample: int = 2748, reps: int = 5):
 
 
 def cpu_block_extrapolation(reps: int = 3):
-    """CPU leg for BASELINE configs 3-5: one W4A16 AA
+    """CPU leg for the aggregator configurations (S = 8 and 32): one W4A16 AA
     block on the host in the reference's semantics (numpy dequantisation of
     its four linears, torch fp32 LayerNorm / matmuls / SDPA / GELU; q/k-norm
     and RoPE left out, under 1 % of the work), timed as a frame block at
