@@ -28,6 +28,8 @@
 // would otherwise evict the weight matrix and the activation rows that the
 // other tiles of the XCD still read from its L2 (fc1 at M = 10992: HBM reads
 // 94.7 -> 43.0 MB per launch).
+#include <type_traits>
+
 #include "w4a16_common.h"
 
 namespace qv {
@@ -45,7 +47,11 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   constexpr int BM = 32 * MT, NT = 2;
   constexpr int A_BYTES = BM * 128;
   constexpr int STAGE = SUB * A_BYTES;
-  constexpr int NSTAGE = 3;
+  // VMEM instructions of one stage's weight loads (load_b), and the wait at a
+  // stage's end that leaves exactly those of the stage two ahead in flight
+  constexpr int W_OPS = SUB * NT + 2 * NT;
+  static_assert(W_OPS < 16, "vmcnt immediate");
+  constexpr int WAIT_NEXT = 0x0F70 | W_OPS;
   constexpr int A_INSTR = BM / 32;                // 1 KB direct loads per wave for A
   static_assert(SUB * A_INSTR < 16, "vmcnt immediate");
   static_assert(SUB == 1 || SUB == 2, "64- or 128-k stages");
@@ -160,8 +166,9 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
       if (t < T - 1) {
         dq((t + 1) & 3, wq[(t + 1) >> 2], sv, zv, wf[(t + 1) & 1]);
       } else {
-        // the next stage's weights (and every copy issued before them) have landed
-        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        // the next stage's weights and every copy issued before this
+        // stage's own weight loads have landed
+        __builtin_amdgcn_s_waitcnt(WAIT_NEXT);
         dq(0, nwq[0], nsv, nzv, wf[0]);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -172,45 +179,55 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
     for (int j = 0; j < NT; ++j) wf0[j] = wf[0][j];
   };
 
-  // Stage i = ks - k0 uses LDS buffer i % 3 and weight register set i & 1.
+  // Stage i = ks - k0 uses LDS buffer i % 3 and weight register set i % 3.
   // Per stage: barrier (every wave is done reading buffer (i + 2) % 3, the
   // previous stage's, and sees A(ks + 1)), the copy of A(ks + 2) into that
-  // buffer, the weight loads B(ks + 1) into the idle register set, then the
-  // stage's compute, whose last step waits for all of this wave's loads
-  // (vmcnt(0): A(ks + 2) was issued before B(ks + 1), so it is no extra wait)
-  // and reads stage ks + 1's first fragments -- A(ks + 1) landed at the same
-  // point of the previous stage, before the barrier that published it.  The
-  // A copies are inline asm the compiler does not count; the compiler's own
-  // wait for B(ks + 1) is that same vmcnt(0).  k0 and k1 are even (whole
-  // 128-k groups), so every iteration runs two stages.  Loads past k1 - 1
-  // repeat stage k1 - 1 (valid addresses; A into a buffer nobody reads, B into
-  // a dead register set), so every stage issues the same count.  (An odd
-  // stage count, with a conditional second half, made the compiler spill the
-  // accumulators in a kernel that loops over tiles.)
-  uint4 wq0[SUB][NT], wq1[SUB][NT];
-  uint32_t sv0[NT], zv0[NT], sv1[NT], zv1[NT];
+  // buffer, the weight loads B(ks + 2) into register set (i + 2) % 3, then
+  // the stage's compute, whose last step waits for every load but those of
+  // B(ks + 2) (vmcnt(W_OPS): A(ks + 2) and B(ks + 1) have landed) and reads
+  // stage ks + 1's first fragments -- A(ks + 1) landed at the same point of
+  // the previous stage, before the barrier that published it.  So a stage's
+  // weights are requested about two stages before their first use, where
+  // one stage (two register sets) left their latency exposed: fc1 at
+  // M = 10992 95.7 -> 92.6 us, qkv 67.2 -> 65.6 us, config-1 qkv 14.2 ->
+  // 13.6 us, the K split at 1374 x 4096 -> 1024 26.9 -> 25.1 us (same box,
+  // bit-identical).  The A copies are inline asm the compiler does not
+  // count; its own waits for B(ks + 1), by its count of weight loads alone,
+  // are no later than that vmcnt(W_OPS).  Three stages run per iteration, so
+  // every register-set index is a constant; a remainder of one or two stages
+  // runs after the loop.  Loads past k1 - 1 repeat stage k1 - 1 (valid
+  // addresses; A into a buffer nobody reads, B into a dead register set), so
+  // every stage issues the same count.
+  uint4 wq[3][SUB][NT];
+  uint32_t sv[3][NT], zv[3][NT];
   uint4 af0[MT], wf0[NT];
   // stage indices in units of SUB x 64 k
   const int L0 = k0 / SUB, L1 = k1 / SUB;
   const int last = L1 - 1, nks = L1 - L0;
   issue(L0, 0);
   issue(L0 + 1 < L1 ? L0 + 1 : last, 1);
-  load_b(L0, wq0, sv0, zv0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): A(k0), A(k0 + 1), B(k0)
+  load_b(L0, wq[0], sv[0], zv[0]);
+  load_b(L0 + 1 < L1 ? L0 + 1 : last, wq[1], sv[1], zv[1]);
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): A(k0), A(k0 + 1), B(k0), B(k0 + 1)
   lds_barrier();
   read_a(0, 0, 0, af0);
-  dq(0, wq0[0], sv0, zv0, wf0);
-  for (int i = 0; i < nks; i += 2) {
-    const int ks = L0 + i;
+  dq(0, wq[0][0], sv[0], zv[0], wf0);
+  auto stage = [&](int s, auto pc) __attribute__((always_inline)) {
+    constexpr int p = decltype(pc)::value, p1 = (p + 1) % 3, p2 = (p + 2) % 3;
     lds_barrier();
-    issue(ks + 2 < L1 ? ks + 2 : last, (i + 2) % NSTAGE);
-    load_b(ks + 1, wq1, sv1, zv1);
-    compute(i % NSTAGE, (i + 1) % NSTAGE, wq0, sv0, zv0, wq1, sv1, zv1, af0, wf0);
-    lds_barrier();
-    issue(ks + 3 < L1 ? ks + 3 : last, (i + 3) % NSTAGE);
-    load_b(ks + 2 < L1 ? ks + 2 : last, wq0, sv0, zv0);
-    compute((i + 1) % NSTAGE, (i + 2) % NSTAGE, wq1, sv1, zv1, wq0, sv0, zv0, af0, wf0);
+    const int s2 = s + 2 < L1 ? s + 2 : last;
+    issue(s2, p2);
+    load_b(s2, wq[p2], sv[p2], zv[p2]);
+    compute(p, p1, wq[p], sv[p], zv[p], wq[p1], sv[p1], zv[p1], af0, wf0);
+  };
+  int i = 0;
+  for (; i + 3 <= nks; i += 3) {
+    stage(L0 + i, std::integral_constant<int, 0>());
+    stage(L0 + i + 1, std::integral_constant<int, 1>());
+    stage(L0 + i + 2, std::integral_constant<int, 2>());
   }
+  if (i < nks) stage(L0 + i, std::integral_constant<int, 0>());
+  if (i + 1 < nks) stage(L0 + i + 1, std::integral_constant<int, 1>());
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the repeated loads may not land during the epilogue
 }
 
