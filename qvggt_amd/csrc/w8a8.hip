@@ -29,6 +29,8 @@
 // (OUT 3, qv_w8a8_gemm_residual) reads the residual row chunk and LayerScale
 // gamma in the store loop and writes residual + gamma * fp16(epilogue) in
 // place, which replaces torch's x.addcmul_(o, gamma) pass of a VGGT block.
+#include <type_traits>
+
 #include "common.h"
 
 #pragma clang fp contract(off)
@@ -182,38 +184,55 @@ void w8a8_gemm_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b
       mfmas(bw, 1, a1);
       __builtin_amdgcn_sched_barrier(0);
     };
-    // Stage ks uses LDS buffer ks % 3 and weight register set ks & 1.  At its
-    // top: vmcnt(0) lands this wave's activation copy of stage ks + 1 (issued
-    // one stage earlier) and its weights of stage ks; the barrier publishes the
-    // copies and frees buffer (ks + 2) % 3 for stage ks + 2; the weights of stage
-    // ks + 1 go into the idle register set.  Every iteration runs two stages (a
-    // conditional second half made the compiler spill the accumulators); with
-    // an odd stage count the last one multiplies zero weights, which adds
-    // exactly nothing (int8 x 0) whatever stale activations its buffer holds.
-    uint4 bX[NT][2], bY[NT][2];
+    // Stage s uses LDS buffer s % 4 and weight register set s % 3.  At its
+    // top, vmcnt(A_INSTR + W_OPS) lands this wave's activation copy of stage
+    // s + 1 and its weights of stage s, both issued two stages earlier (only
+    // the previous stage's copy and weight loads stay in flight); the barrier
+    // publishes the copies and frees buffer (s + 3) % 4, the previous stage's,
+    // which receives stage s + 3, and the weights of stage s + 2 go into the
+    // register set stage s - 1 used.  Requests one stage ahead (3 buffers, 2
+    // register sets) left their latency exposed: same-box A/B, bit-identical,
+    // fc1 at 10,992 tokens 60.2 -> 57.1 us, fc2 54.7 -> 52.7 us, qkv 47.9 ->
+    // 46.0 us, 2748 x 4096 -> 1024 35.5 -> 21.3 us.  Three stages run per
+    // iteration (constant register-set indices), a remainder of one or two
+    // after the loop; loads past the last stage repeat it (valid addresses,
+    // into a buffer or register set nobody reads), so every stage issues the
+    // same count and the wait above stays exact.
+    constexpr int NB = 4;                      // LDS buffers of the activation copies
+    constexpr int W_OPS = 2 * NT;              // weight loads per stage
+    constexpr int WAIT_TOP = 0x0F70 | (A_INSTR + W_OPS);
+    static_assert(A_INSTR + W_OPS < 16, "vmcnt immediate");
+    static_assert(NB * STAGE <= LDS_BYTES, "the activation buffers fit the LDS allocation");
+    uint4 bw3[3][NT][2];
+    const int last = KS - 1;
     issue(0, 0);
-    if (KS > 1) issue(1, 1);
-    load_b(0, bX);
+    issue(KS > 1 ? 1 : last, 1);
+    issue(KS > 2 ? 2 : last, 2);
+    load_b(0, bw3[0]);
+    load_b(KS > 1 ? 1 : last, bw3[1]);
     __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0), as in the LDS path
     lds_barrier();
     read_a(0, 0, a0);
-    for (int ks = 0; ks < KS; ks += 2) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-      lds_barrier();
-      if (ks + 2 < KS) issue(ks + 2, (ks + 2) % NSTAGE);
-      if (ks + 1 < KS) {
-        load_b(ks + 1, bY);
-      } else {
-#pragma unroll
-        for (int j = 0; j < NT; ++j) bY[j][0] = bY[j][1] = make_uint4(0, 0, 0, 0);
+    auto stage = [&](int s, auto pc) __attribute__((always_inline)) {
+      constexpr int p = decltype(pc)::value, p2 = (p + 2) % 3;
+      if (s > 0) {
+        __builtin_amdgcn_s_waitcnt(WAIT_TOP);   // A(s + 1), B(s): issued two stages ago
+        lds_barrier();
       }
-      compute(ks % NSTAGE, (ks + 1) % NSTAGE, bX);
-      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-      lds_barrier();
-      if (ks + 3 < KS) issue(ks + 3, (ks + 3) % NSTAGE);
-      if (ks + 2 < KS) load_b(ks + 2, bX);
-      compute((ks + 1) % NSTAGE, (ks + 2) % NSTAGE, bY);
+      const int s3 = s + 3 < KS ? s + 3 : last, s2 = s + 2 < KS ? s + 2 : last;
+      issue(s3, (s + 3) & (NB - 1));
+      load_b(s2, bw3[p2]);
+      compute(s & (NB - 1), (s + 1) & (NB - 1), bw3[p]);
+    };
+    int i = 0;
+    for (; i + 3 <= KS; i += 3) {
+      stage(i, std::integral_constant<int, 0>());
+      stage(i + 1, std::integral_constant<int, 1>());
+      stage(i + 2, std::integral_constant<int, 2>());
     }
+    if (i < KS) stage(i, std::integral_constant<int, 0>());
+    if (i + 1 < KS) stage(i + 1, std::integral_constant<int, 1>());
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the repeated loads land before the epilogue
   } else {
     // Fragments of k-step s of the stage in LDS buffer st (weights, activations).
     auto read = [&](int st, int s, uint4 (&bw)[NT], uint4 (&av)[MT]) {
