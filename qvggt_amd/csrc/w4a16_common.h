@@ -69,6 +69,31 @@ __device__ __forceinline__ uint4 dq_frag(const uint4& wq, uint32_t s_bits, uint3
   return r;
 }
 
+// dq_frag with the scale and scaled zero as 32-bit words holding two
+// channels' 16-bit values; sel (a v_perm_b32 byte selector, 0x01000100 or
+// 0x03020302) picks this lane's half and splats it.
+template <bool BF16, int t>
+__device__ __forceinline__ uint4 dq_frag_w(const uint4& wq, uint32_t s_word, uint32_t z_word, uint32_t sel) {
+  const uint32_t s_sp = __builtin_amdgcn_perm(s_word, s_word, sel), z_sp = __builtin_amdgcn_perm(z_word, z_word, sel);
+  uint4 r;
+  if constexpr (!BF16) {
+    const f16x2 s2 = __builtin_bit_cast(f16x2, s_sp);
+    const f16x2 z2 = __builtin_bit_cast(f16x2, z_sp);
+    r.x = dq_pair_f16<t>(wq.x, wq.x >> 8, s2, z2);
+    r.y = dq_pair_f16<t>(wq.y, wq.y >> 8, s2, z2);
+    r.z = dq_pair_f16<t>(wq.z, wq.z >> 8, s2, z2);
+    r.w = dq_pair_f16<t>(wq.w, wq.w >> 8, s2, z2);
+  } else {
+    const float s = __builtin_bit_cast(float, s_sp << 16);
+    const float z = __builtin_bit_cast(float, z_sp << 16);
+    r.x = dq_pair_bf16<t>(wq.x, s, z);
+    r.y = dq_pair_bf16<t>(wq.y, s, z);
+    r.z = dq_pair_bf16<t>(wq.z, s, z);
+    r.w = dq_pair_bf16<t>(wq.w, s, z);
+  }
+  return r;
+}
+
 template <bool BF16>
 __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c) {
   if constexpr (BF16) {
