@@ -39,9 +39,10 @@ constexpr int EP = 128;  // bytes per staged epilogue row (64 fp16, chunk-swizzl
 // Main loop of one tile over its 64-k stages [k0, k1): acc += the tile's
 // products (acc is not cleared here).  Returns with every load landed.
 // MID: the k-step of a stage after which the stage's weight requests (for
-// the stage two ahead) are issued; -1 issues them at the stage top, right
-// after the activation copy.
-template <bool BF16, int MT, int SUB = 1, int MID = -1>
+// the stage two ahead) are issued; -1 issues them at the stage top.  ADMA
+// likewise for the activation copy of the stage two ahead (ADMA <= MID: the
+// copy precedes the weight requests).
+template <bool BF16, int MT, int SUB = 1, int MID = -1, int ADMA = -1>
 __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const uint16_t* __restrict__ x,
                                                 const uint32_t* __restrict__ qw,
                                                 const uint16_t* __restrict__ scales,
@@ -155,9 +156,9 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   // fences keep the compiler from sinking the reads next to their use.
   auto compute = [&](int st, int nst, const uint4 (&wq)[SUB][NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT],
                      const uint4 (&nwq)[SUB][NT], const uint32_t (&nsv)[NT], const uint32_t (&nzv)[NT], uint4 (&af0)[MT],
-                     uint4 (&wf0)[NT], auto&& mid) {
+                     uint4 (&wf0)[NT], auto&& mid, auto&& mida) {
     constexpr int T = 4 * SUB;   // k-steps per stage
-    static_assert(MID < T - 1, "the weight requests precede the stage's last k-step");
+    static_assert(MID < T - 1 && ADMA <= MID, "the activation copy, then the weight requests, before the last k-step");
     uint4 af[2][MT], wf[2][NT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[0][i] = af0[i];
@@ -175,6 +176,7 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
       }
       if (t < T - 1) {
         dq((t + 1) & 3, wq[(t + 1) >> 2], sv, zv, wf[(t + 1) & 1]);
+        if (t == ADMA) mida();
         if (t == MID) mid();
       } else {
         // the next stage's weights and every copy issued before this
@@ -227,10 +229,11 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
     constexpr int p = decltype(pc)::value, p1 = (p + 1) % 3, p2 = (p + 2) % 3;
     lds_barrier();
     const int s2 = s + 2 < L1 ? s + 2 : last;
-    issue(s2, p2);
+    auto req_a = [&]() __attribute__((always_inline)) { issue(s2, p2); };
+    if constexpr (ADMA < 0) req_a();
     auto req_b = [&]() __attribute__((always_inline)) { load_b(s2, wq[p2], sv[p2], zv[p2]); };
     if constexpr (MID < 0) req_b();
-    compute(p, p1, wq[p], sv[p], zv[p], wq[p1], sv[p1], zv[p1], af0, wf0, req_b);
+    compute(p, p1, wq[p], sv[p], zv[p], wq[p1], sv[p1], zv[p1], af0, wf0, req_b, req_a);
   };
   int i = 0;
   for (; i + 3 <= nks; i += 3) {
@@ -436,7 +439,7 @@ __device__ __forceinline__ void stream_epilogue(uint8_t* __restrict__ lds, const
 }
 
 // One whole tile: logical tile lid of the rows from m_base.
-template <bool BF16, int MT, int EPI, int SUB = 1, int MID = -1>
+template <bool BF16, int MT, int EPI, int SUB = 1, int MID = -1, int ADMA = -1>
 __device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uint16_t* __restrict__ x,
                                             const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scales,
                                             const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ bias,
@@ -451,7 +454,7 @@ __device__ __forceinline__ void stream_tile(uint8_t* __restrict__ lds, const uin
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
-  stream_mainloop<BF16, MT, SUB, MID>(lds, x, qw, scales, zeros, M, N, K, m0, n0, 0, K >> 6, acc);
+  stream_mainloop<BF16, MT, SUB, MID, ADMA>(lds, x, qw, scales, zeros, M, N, K, m0, n0, 0, K >> 6, acc);
   stream_epilogue<BF16, MT, EPI>(lds, bias, gamma, out, M, N, qk, m0, n0, acc);
 }
 
@@ -477,12 +480,19 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
   // tiles: 85.5 -> 87.1 us; 8244 x 4096 -> 1024 71.7 -> 74.9 us), whose
   // stages are half as long; those keep the requests at the stage top.
   constexpr int MID = (MT2 == 2 || (MT <= 2 && SUB == 1)) ? -1 : 1;
+  // The activation copy after the first k-step instead of at the stage top
+  // (0.75 of a stage ahead of use): 1-4 % faster for one-round 128-k stages
+  // (2748 x 1024 -> 1024 11.0 -> 10.6 us, 1000 x 1024 -> 3072 10.8 -> 10.6
+  // us; config-1 qkv +2.5 % and +0.1 % in two runs) and one-range 96-row
+  // tiles (proj at M = 10992 +0.6-2 %), within 1 % for 128-row tiles, 2-7 %
+  // slower with 64-row 64-k tiles.
+  constexpr int ADMA = (SUB == 2 || (MT2 == 0 && MT == 3)) ? 0 : -1;
   const int b = blockIdx.x;
   if (MT2 == 0 || b < n_first) {
-    stream_tile<BF16, MT, EPI, SUB, MID>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
+    stream_tile<BF16, MT, EPI, SUB, MID, ADMA>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
                                xcd_remap(b, MT2 == 0 ? (int)gridDim.x : n_first), 0);
   } else {
-    stream_tile<BF16, (MT2 > 0 ? MT2 : 1), EPI, 1, MID>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
+    stream_tile<BF16, (MT2 > 0 ? MT2 : 1), EPI, 1, MID, ADMA>(lds, x, qw, scales, zeros, bias, gamma, out, M, N, K, tiles_n, qk,
                                                 xcd_remap(b - n_first, (int)gridDim.x - n_first), m_split);
   }
 }
@@ -525,10 +535,11 @@ void w4a16_ksplit_kernel(const uint16_t* __restrict__ x, const uint32_t* __restr
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
-  // weight requests after each stage's second k-step (as in stream_tile;
-  // measured faster for every tile height here: 1374 x 4096 -> 1024 24.8 ->
-  // 23.6 us, 2748 x 4096 -> 1024 31.2 -> 30.2 us)
-  stream_mainloop<BF16, MT, 1, 1>(lds + grp * (3 * BM * 128), x, qw, scales, zeros, M, N, K, m0, n0, grp * half,
+  // weight requests after each stage's second k-step and the activation copy
+  // after its first (as in stream_tile; measured faster for every tile height
+  // here: 1374 x 4096 -> 1024 24.8 -> 23.6 -> 23.6 us, 2748 x 4096 -> 1024
+  // 31.2 -> 30.2 -> 29.4 us)
+  stream_mainloop<BF16, MT, 1, 1, 0>(lds + grp * (3 * BM * 128), x, qw, scales, zeros, M, N, K, m0, n0, grp * half,
                             (grp + 1) * half, acc);
   // every wave is done reading its group's stage buffers
   lds_barrier();
