@@ -53,7 +53,8 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   constexpr int STAGE = SUB * A_BYTES;
   // VMEM instructions of one stage's weight loads (load_b), and the wait at a
   // stage's end that leaves exactly those of the stage two ahead in flight
-  constexpr int W_OPS = SUB * NT + 2 * NT;
+  constexpr int W_OPS = SUB * NT;
+  constexpr int SCL = 3 * STAGE;   // the stages' scale / zero rows: 3 x 1 KB after the activation stages
   static_assert(W_OPS < 16, "vmcnt immediate");
   constexpr int WAIT_NEXT = 0x0F70 | W_OPS;
   constexpr int A_INSTR = BM / 32;                // 1 KB direct loads per wave for A
@@ -90,24 +91,26 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   // segment of packed row n/4 (one 1 KB instruction covers 8 whole segments);
   // S / Z: the 32-bit word holding the channel's 16-bit scale (scaled zero)
   // of the stage's group and its even / odd neighbour's; dq_frag_w picks the
-  // half.  Word loads measured 0.2-2 % faster than 16-bit loads of the same
-  // values on every shape (fc1 93.6 -> 93.4 us, 2748 x 4096 -> 1024 31.1 ->
-  // 30.4 us; same box, bit-identical).
+  // half.  The workgroup's 256-channel row of each table comes with the
+  // stage's activation copy (one 256-byte LDS DMA per wave) into a 3 x 1 KB
+  // ring after the stages, and each lane reads its two words from there:
+  // the per-lane 32-bit global loads this replaces (which measured 0.2-2 %
+  // faster than 16-bit ones) cost 0-2 % on the multi-round shapes and 2-7 %
+  // on one-round ones (1374 x 4096 -> 1024 24.95 -> 23.43 us, proj at
+  // M = 10992 25.3 -> 24.8 us; same box, bit-identical).
   uint32_t b_voff[NT], sz_voff[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
     const int n = 64 * wave + 32 * j + l32;
     b_voff[j] = (uint32_t)((n >> 2) * K2 + 32 * (n & 3) + 16 * h);
-    sz_voff[j] = (uint32_t)((n & ~1) * 2);
+    sz_voff[j] = (uint32_t)((n & ~1) * 2);   // byte offset of the channel's word in a 512-byte row
   }
-  auto load_b = [&](int ks, uint4 (&wq)[SUB][NT], uint32_t (&sv)[NT], uint32_t (&zv)[NT]) {
+  auto load_b = [&](int ks, uint4 (&wq)[SUB][NT]) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
 #pragma unroll
       for (int u = 0; u < SUB; ++u)
         wq[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsB, b_voff[j], (SUB * ks + u) * 128, 0));
-      sv[j] = __builtin_amdgcn_raw_buffer_load_b32(rsS, sz_voff[j], ((SUB * ks) >> 1) * N * 2, 0);
-      zv[j] = __builtin_amdgcn_raw_buffer_load_b32(rsZ, sz_voff[j], ((SUB * ks) >> 1) * N * 2, 0);
     }
   };
 
@@ -121,6 +124,18 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
         const int r0 = 8 * (A_INSTR * wave + q);
         lds_dma16(rsA, a_voff[(r0 >> 3) & 1], r0 * K2 + (SUB * ks + u) * 128, base + r0 * 128);
       }
+    }
+    // the stage's group row of the workgroup's 256 scales (waves 0, 1) and
+    // scaled zeros (waves 2, 3), 256 bytes per wave, into ring entry st
+    lds_dma4(wave < 2 ? rsS : rsZ, (uint32_t)((64 * (wave & 1) + lane) * 4), (uint32_t)(((SUB * ks) >> 1) * N * 2),
+             lds0 + SCL + st * 1024 + wave * 256);
+  };
+  auto read_s = [&](int st, uint32_t (&sv)[NT], uint32_t (&zv)[NT]) {
+    const uint8_t* base = lds + SCL + st * 1024;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      sv[j] = *reinterpret_cast<const uint32_t*>(base + sz_voff[j]);
+      zv[j] = *reinterpret_cast<const uint32_t*>(base + 512 + sz_voff[j]);
     }
   };
 
@@ -155,7 +170,7 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   // dequantisation; af0 / wf0 hold those fragments on exit.  The scheduling
   // fences keep the compiler from sinking the reads next to their use.
   auto compute = [&](int st, int nst, const uint4 (&wq)[SUB][NT], const uint32_t (&sv)[NT], const uint32_t (&zv)[NT],
-                     const uint4 (&nwq)[SUB][NT], const uint32_t (&nsv)[NT], const uint32_t (&nzv)[NT], uint4 (&af0)[MT],
+                     const uint4 (&nwq)[SUB][NT], uint32_t (&nsv)[NT], uint32_t (&nzv)[NT], uint4 (&af0)[MT],
                      uint4 (&wf0)[NT], auto&& mid, auto&& mida) {
     constexpr int T = 4 * SUB;   // k-steps per stage
     static_assert(MID < T - 1 && ADMA <= MID, "the activation copy, then the weight requests, before the last k-step");
@@ -166,8 +181,12 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
     for (int j = 0; j < NT; ++j) wf[0][j] = wf0[j];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      if (t < T - 1) read_a(st, (t + 1) >> 2, (t + 1) & 3, af[(t + 1) & 1]);
-      else read_a(nst, 0, 0, af[0]);
+      if (t < T - 1) {
+        read_a(st, (t + 1) >> 2, (t + 1) & 3, af[(t + 1) & 1]);
+      } else {
+        read_a(nst, 0, 0, af[0]);
+        read_s(nst, nsv, nzv);
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
@@ -212,18 +231,19 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
   // addresses; A into a buffer nobody reads, B into a dead register set), so
   // every stage issues the same count.
   uint4 wq[3][SUB][NT];
-  uint32_t sv[3][NT], zv[3][NT];
+  uint32_t sv[3][NT], zv[3][NT];   // scale / zero words, read from the ring
   uint4 af0[MT], wf0[NT];
   // stage indices in units of SUB x 64 k
   const int L0 = k0 / SUB, L1 = k1 / SUB;
   const int last = L1 - 1, nks = L1 - L0;
   issue(L0, 0);
   issue(L0 + 1 < L1 ? L0 + 1 : last, 1);
-  load_b(L0, wq[0], sv[0], zv[0]);
-  load_b(L0 + 1 < L1 ? L0 + 1 : last, wq[1], sv[1], zv[1]);
+  load_b(L0, wq[0]);
+  load_b(L0 + 1 < L1 ? L0 + 1 : last, wq[1]);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): A(k0), A(k0 + 1), B(k0), B(k0 + 1)
   lds_barrier();
   read_a(0, 0, 0, af0);
+  read_s(0, sv[0], zv[0]);
   dq(0, wq[0][0], sv[0], zv[0], wf0);
   auto stage = [&](int s, auto pc) __attribute__((always_inline)) {
     constexpr int p = decltype(pc)::value, p1 = (p + 1) % 3, p2 = (p + 2) % 3;
@@ -231,7 +251,7 @@ __device__ __forceinline__ void stream_mainloop(uint8_t* __restrict__ lds, const
     const int s2 = s + 2 < L1 ? s + 2 : last;
     auto req_a = [&]() __attribute__((always_inline)) { issue(s2, p2); };
     if constexpr (ADMA < 0) req_a();
-    auto req_b = [&]() __attribute__((always_inline)) { load_b(s2, wq[p2], sv[p2], zv[p2]); };
+    auto req_b = [&]() __attribute__((always_inline)) { load_b(s2, wq[p2]); };
     if constexpr (MID < 0) req_b();
     compute(p, p1, wq[p], sv[p], zv[p], wq[p1], sv[p1], zv[p1], af0, wf0, req_b, req_a);
   };
@@ -512,7 +532,10 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
                            uint16_t* __restrict__ out, int M, int N, int K, int tiles_n, QkRopeArgs qk,
                            int n_first, int m_split) {
   constexpr int MTX = MT > MT2 ? MT : MT2;
-  constexpr int LDS_B = (SUB == 2 ? 6 : 4) * 32 * MTX * 128;   // max(3 stages, the epilogue staging)
+  // max(3 stages + their 3 KB scale / zero ring, the epilogue staging)
+  constexpr int LDS_B = (SUB == 2 ? 6 : 4) * 32 * MTX * 128 > 3 * SUB * 32 * MTX * 128 + 3072
+                            ? (SUB == 2 ? 6 : 4) * 32 * MTX * 128
+                            : 3 * SUB * 32 * MTX * 128 + 3072;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_B];
   // Weight requests after a stage's second k-step (1.5 stages ahead of use)
   // measured 1-4 % faster than at the stage top for 96- and 128-row tiles and
@@ -553,7 +576,7 @@ void w4a16_stream32_kernel(const uint16_t* __restrict__ x, const uint32_t* __res
 // also takes part in the epilogue's opening barrier, after which it is done.
 template <int MT>
 constexpr int ksplit_lds_bytes() {
-  constexpr int stages = 2 * 3 * 32 * MT * 128, part = 32 * MT * 256 * 4, stage_out = 4 * 32 * MT * EP;
+  constexpr int stages = 2 * (3 * 32 * MT * 128 + 3072), part = 32 * MT * 256 * 4, stage_out = 4 * 32 * MT * EP;
   return stages > part ? (stages > stage_out ? stages : stage_out) : (part > stage_out ? part : stage_out);
 }
 
@@ -577,7 +600,7 @@ void w4a16_ksplit_kernel(const uint16_t* __restrict__ x, const uint32_t* __restr
   // after its first (as in stream_tile; measured faster for every tile height
   // here: 1374 x 4096 -> 1024 24.8 -> 23.6 -> 23.6 us, 2748 x 4096 -> 1024
   // 31.2 -> 30.2 -> 29.4 us)
-  stream_mainloop<BF16, MT, 1, 1, 0>(lds + grp * (3 * BM * 128), x, qw, scales, zeros, M, N, K, m0, n0, grp * half,
+  stream_mainloop<BF16, MT, 1, 1, 0>(lds + grp * (3 * BM * 128 + 3072), x, qw, scales, zeros, M, N, K, m0, n0, grp * half,
                             (grp + 1) * half, acc);
   // every wave is done reading its group's stage buffers
   lds_barrier();
