@@ -28,9 +28,10 @@
 //    registers 8p..8p+7 of block kb, i.e. keys 32kb + 16p + {0..3, 8..11} + 4h.
 //  * K and V tiles arrive by LDS DMA in their natural [key][dim] layout
 //    (128-byte rows; 16-byte chunk c of row r at c ^ fk(r) for K and
-//    c ^ fv(r) for V), one DMA tile of 128 keys ahead; each DMA tile is
-//    consumed as two 64-key compute tiles, so the workgroup meets at one
-//    barrier per 128 keys (1-2 % faster than one per 64, bit-identical).
+//    c ^ fv(r) for V), one DMA tile ahead.  In the 4-wave form a DMA tile
+//    holds 128 keys, consumed as two 64-key compute tiles, so the workgroup
+//    meets at one barrier per 128 keys (1-2 % faster than one per 64,
+//    bit-identical); the 2-wave form copies 64-key tiles.
 //  * V^T (the PV A operand) comes out of LDS through ds_read_b64_tr_b16: two
 //    transposed 8-byte reads give each lane its dim's 8 keys in k-slot order,
 //    with no register staging or transposed stores.
@@ -39,12 +40,16 @@
 namespace qv {
 
 constexpr int ATT_QW = 64;                 // queries per wave (two 32-query blocks)
-constexpr int ATT_WAVES = 4;               // waves per workgroup
-constexpr int ATT_BQ = ATT_WAVES * ATT_QW; // queries per workgroup
 constexpr int ATT_BK = 64;                 // keys per compute tile
-constexpr int ATT_SUB = 2;                 // compute tiles per DMA tile (one barrier per DMA tile)
-constexpr int ATT_BKD = ATT_BK * ATT_SUB;  // keys per DMA tile
-constexpr int ATT_DMA = ATT_BKD / 8 / ATT_WAVES;  // 1 KB (8-key) DMA rows per wave per DMA tile, K and V each
+// The kernel's two forms (template WAVES, SUB): 4 waves per workgroup with
+// 128-key DMA tiles (64 KB of K / V buffers, two workgroups per CU), and, for
+// launches that would not fill one round of those, 2 waves with 64-key DMA
+// tiles (32 KB, four workgroups per CU), which spreads the queries over twice
+// as many workgroups (bit-identical: the key order of every query is the
+// same; 4 x 1374 frame tokens 0.5-5 % and one 5496-token sequence 1.8 %
+// faster, two boxes).  At 8 x 1374 (1.5 rounds of the 4-wave form) the
+// 2-wave form was 7-8 % slower: twice the K / V copies per query and a
+// barrier per 64 keys.
 
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units: P <= 256 between rescales
 constexpr float P_SUM_LIMIT = 256.0f;  // 2^RESCALE_SLACK: a lane's tile sum above it may hide a P above it
@@ -88,9 +93,16 @@ __device__ __forceinline__ float half_sum(float x) {
   return a + b;
 }
 
-__global__ __launch_bounds__(64 * ATT_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(
+template <int WAVES, int SUB>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     uint16_t* __restrict__ out, int L, int H, long q_ts, long kv_ts, long v_ts, long o_ts, float scale_log2) {
+  constexpr int ATT_WAVES = WAVES;               // waves per workgroup
+  constexpr int ATT_BQ = ATT_WAVES * ATT_QW;     // queries per workgroup
+  constexpr int ATT_SUB = SUB;                   // compute tiles per DMA tile (one barrier per DMA tile)
+  constexpr int ATT_BKD = ATT_BK * ATT_SUB;      // keys per DMA tile
+  constexpr int ATT_DMA = ATT_BKD / 8 / ATT_WAVES;  // 1 KB (8-key) DMA rows per wave per DMA tile, K and V each
+  static_assert(ATT_DMA * 8 * ATT_WAVES == ATT_BKD, "DMA rows split evenly over the waves");
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[2][ATT_BKD * 128];
   __shared__ __attribute__((aligned(1024))) uint8_t v_lds[2][ATT_BKD * 128];
 
@@ -375,13 +387,23 @@ extern "C" int qv_attention_fwd(const void* q, const void* k, const void* v, voi
                "q, k, v must be 16-byte and out 8-byte aligned");
   QV_CHECK_ARG((uint64_t)L * k_token_stride * 2 < (1ull << 32) && (uint64_t)L * v_token_stride * 2 < (1ull << 32),
                "sequence too long for 32-bit offsets");
-  const long qtiles = (L + qv::ATT_BQ - 1) / qv::ATT_BQ;
-  const long nwg = B * H * qtiles;
+  // 4-wave workgroups (256 queries) when they fill at least one round of
+  // the 512 workgroup slots (two per CU); else 2-wave workgroups
+  const long qtiles4 = (L + 4 * qv::ATT_QW - 1) / (4 * qv::ATT_QW);
+  const bool wide = B * H * qtiles4 >= 512;
+  const long bq = wide ? 4 * qv::ATT_QW : 2 * qv::ATT_QW;
+  const long nwg = B * H * ((L + bq - 1) / bq);
   QV_CHECK_ARG(nwg <= INT32_MAX, "grid too large");
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(qv::attention_fwd_kernel, dim3((unsigned)nwg), dim3(64 * qv::ATT_WAVES), 0, (hipStream_t)stream,
-                     (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out, (int)L, (int)H,
-                     (long)q_token_stride, (long)k_token_stride, (long)v_token_stride, (long)out_token_stride,
-                     scale_log2);
+#define QV_ATT_ARGS                                                                                       \
+  (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)out, (int)L, (int)H, (long)q_token_stride, \
+      (long)k_token_stride, (long)v_token_stride, (long)out_token_stride, scale_log2
+  if (wide)
+    hipLaunchKernelGGL((qv::attention_fwd_kernel<4, 2>), dim3((unsigned)nwg), dim3(256), 0, (hipStream_t)stream,
+                       QV_ATT_ARGS);
+  else
+    hipLaunchKernelGGL((qv::attention_fwd_kernel<2, 1>), dim3((unsigned)nwg), dim3(128), 0, (hipStream_t)stream,
+                       QV_ATT_ARGS);
+#undef QV_ATT_ARGS
   return qv::check_launch("attention_fwd");
 }
