@@ -58,6 +58,27 @@ def test_global_attention_s32_sampled_rows(gpu):
     assert np.abs(got - ref).max() / np.abs(ref).max() <= TOL
 
 
+def test_attention_two_forms_agree_bitwise(gpu):
+    """Launches that would not fill one round of 4-wave workgroups run the
+    2-wave form (64-key DMA tiles); every query sees its keys in the same
+    order in both forms, so the first 4 frames of an 8-frame launch (4-wave
+    form) equal a 4-frame launch on the same tokens (2-wave form) bit for bit,
+    and both meet the oracle."""
+    from qvggt_amd import awq_inference_engine as E
+    L, H = 1374, 16
+    x = _qkv(8 * L, H, 11)
+    xt = torch.from_numpy(x).to(gpu)
+    out8 = E.attention(xt[:, 0], xt[:, 1], xt[:, 2], L)
+    x4 = xt[:4 * L].contiguous()
+    out4 = E.attention(x4[:, 0], x4[:, 1], x4[:, 2], L)
+    torch.cuda.synchronize()
+    assert torch.equal(out8[:4 * L], out4)
+    rows = np.random.default_rng(2).choice(4 * L, 300, replace=False)
+    ref = attention_ref(x[:4 * L, 0], x[:4 * L, 1], x[:4 * L, 2], 4, L, rows=rows)
+    got = out4.float().cpu().numpy()[rows]
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= TOL
+
+
 def test_attention_separate_buffers_and_determinism(gpu):
     from qvggt_amd import awq_inference_engine as E
     B, L, H = 2, 300, 4
